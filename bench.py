@@ -1,0 +1,287 @@
+"""Benchmark of the MI355X BASED kernels; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--configs all|none]
+
+Headline workload: fused causal BASED forward (la_based_parallel_fwd) at B=2, H=16, N=8192,
+d=16, dv=64, bf16 inputs and output, fp32 accumulation -- one "step" is one full forward
+over that batch, inputs resident in HBM.  ``value`` is TFLOP/s of algorithmic work
+(causal pairs x 2(d+dv) flop); ``roofline`` compares it with the bf16 dense MFMA peak.
+``per_config`` adds ms/call, TFLOP/s and roofline fraction for every benchmark
+configuration (fp32 parallel, bf16 parallel, chunked, sliding, long-context chunked).
+``cpu_baseline`` times the CPU restatement of the reference's PyTorch path on a bounded
+sample of the headline workload, on this host's cores.
+
+GPU time is measured with HIP events on the stream the kernels are launched on, around K
+back-to-back calls after W warm-up calls; HBM-bound configurations rotate through several
+input sets so that repeated calls do not run out of the 256 MB Infinity Cache.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "trainium-linear-attention_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3      # MI355X fp32 matrix
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+
+METRIC = "BASED fwd ms + TFLOP/s at B=2,H=16,N=8192,d=16,dv=64 (% MFMA/HBM roofline)"
+
+# (name, kind, B, H, N, d, dv, dtype, seed, chunk, window, prescale)
+CONFIGS = [
+    ("c1_parallel_fp32", "parallel", 1, 4, 1024, 16, 64, "f32", 0, 64, 64, True),
+    ("c2_parallel_bf16", "parallel", 2, 16, 2048, 16, 64, "bf16", 1, 64, 64, True),
+    ("c3_chunked_bf16", "chunked", 2, 16, 8192, 16, 64, "bf16", 2, 64, 64, True),
+    ("c4_sliding_bf16", "sliding", 2, 16, 4096, 64, 64, "bf16", 3, 64, 64, False),
+    ("c5_chunked_long_bf16", "chunked", 1, 16, 65536, 16, 64, "bf16", 4, 128, 64, True),
+]
+HEADLINE = ("parallel_b2h16n8192", "parallel", 2, 16, 8192, 16, 64, "bf16", 2, 64, 64, True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--rotate", type=int, default=4, help="input sets cycled through for HBM-bound configs")
+    ap.add_argument("--configs", choices=["all", "none"], default="all")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-heads", type=int, default=2)
+    return ap.parse_args()
+
+
+def make_inputs(B, H, N, d, dv, dtype, seed, prescale, device):
+    """Seeded N(0,1) q, k, v drawn on the CPU in the order q, k, v; BASED configurations divide
+    q and k by sqrt(d) (the op then applies its own 1/sqrt(d))."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, N, d, generator=g)
+    k = torch.randn(B, H, N, d, generator=g)
+    v = torch.randn(B, H, N, dv, generator=g)
+    if prescale:
+        q = q / math.sqrt(d)
+        k = k / math.sqrt(d)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    return q.to(tdt).to(device), k.to(tdt).to(device), v.to(tdt).to(device)
+
+
+def feature_dim(d, symmetric=True):
+    return 1 + d + (d * (d + 1) // 2 if symmetric else d * d)
+
+
+def work(kind, B, H, N, d, dv, esz, chunk, window):
+    """Algorithmic FLOP and HBM bytes of one call (q, k, v read once, out written once)."""
+    BH = B * H
+    if kind == "parallel":
+        flop = BH * N * (N + 1) / 2 * 2 * (d + dv)
+    elif kind == "chunked":
+        flop = BH * N * (4 * feature_dim(d, symmetric=False) * dv + (chunk + 1) * (d + dv))
+    else:
+        W = window
+        pairs = sum(min(t + 1, W) for t in range(N)) if N <= 1 << 20 else N * W
+        flop = BH * pairs * 2 * (d + dv)
+    nbytes = BH * N * (2 * d + 2 * dv) * esz
+    return flop, nbytes
+
+
+class Call:
+    """One preallocated kernel launch through the C ABI."""
+
+    def __init__(self, kind, q, k, v, chunk, window, out_f32=False):
+        import torch
+
+        from kernels import _lib
+
+        self.L = _lib.lib()
+        self.kind = kind
+        B, H, N, d = q.shape
+        dv = v.shape[-1]
+        self.args_shape = (B, H, N, d, dv)
+        self.q, self.k, self.v = q, k, v
+        odt = torch.float32 if out_f32 else q.dtype
+        self.out = torch.empty(B, H, N, dv, dtype=odt, device=q.device)
+        self.dt = _lib.dtype_code(q.dtype)
+        self.odt = _lib.dtype_code(odt)
+        self.stream = torch.cuda.current_stream(q.device).cuda_stream
+        self.chunk, self.window = chunk, window
+        self.scale = 1.0 / math.sqrt(d)
+        self.ws = None
+        self.ws_bytes = 0
+        if kind == "chunked":
+            nb = int(self.L.la_based_chunked_workspace_bytes(B, H, N, d, dv, chunk))
+            if nb == (1 << 64) - 1:
+                raise RuntimeError("chunked kernel unsupported for this shape")
+            self.ws_bytes = nb
+            self.ws = torch.empty(max(nb, 1), dtype=torch.uint8, device=q.device)
+        self._check = _lib.check
+
+    def __call__(self):
+        B, H, N, d, dv = self.args_shape
+        L = self.L
+        if self.kind == "parallel":
+            rc = L.la_based_parallel_fwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dt,
+                                         self.out.data_ptr(), self.odt, None, B, H, N, d, dv, self.scale, 1e-6, 1,
+                                         self.stream)
+        elif self.kind == "chunked":
+            rc = L.la_based_chunked_fwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dt,
+                                        self.out.data_ptr(), self.odt, B, H, N, d, dv, self.chunk, self.scale, 1e-6, 1,
+                                        self.ws.data_ptr(), self.ws_bytes, None, self.stream)
+        else:
+            rc = L.la_sliding_window_fwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dt,
+                                         self.out.data_ptr(), self.odt, B, H, N, d, dv, self.window, self.scale,
+                                         self.stream)
+        if rc != 0:
+            self._check(rc, self.kind)
+
+
+def time_calls(calls, steps, warmup):
+    """Mean ms per call over ``steps`` back-to-back launches (HIP events on the launch stream)."""
+    import torch
+
+    for i in range(warmup):
+        calls[i % len(calls)]()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        calls[i % len(calls)]()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def measure(cfg, steps, warmup, rotate, device):
+    name, kind, B, H, N, d, dv, dt, seed, chunk, window, prescale = cfg
+    esz = 2 if dt == "bf16" else 4
+    flop, nbytes = work(kind, B, H, N, d, dv, esz, chunk, window)
+    hbm_bound = kind != "parallel"
+    nsets = rotate if hbm_bound else 1
+    calls = []
+    for r in range(nsets):
+        q, k, v = make_inputs(B, H, N, d, dv, dt, seed + 1000 * r, prescale, device)
+        calls.append(Call(kind, q, k, v, chunk, window))
+    ms = time_calls(calls, steps, warmup)
+    peak = PEAK_BF16_TFLOPS if dt == "bf16" else PEAK_FP32_TFLOPS
+    t_mfma = flop / (peak * 1e12)
+    t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
+    sec = ms * 1e-3
+    res = {
+        "ms": round(ms, 5),
+        "tflops": round(flop / sec / 1e12, 3),
+        "gbs": round(nbytes / sec / 1e9, 1),
+        "bound": "mfma" if t_mfma >= t_hbm else "hbm",
+        "roofline_frac": round(max(t_mfma, t_hbm) / sec, 4),
+        "flop": flop,
+        "bytes": nbytes,
+        "shape": {"B": B, "H": H, "N": N, "d": d, "dv": dv, "dtype": dt, **({"chunk": chunk} if kind == "chunked" else {}),
+                  **({"window": window} if kind == "sliding" else {})},
+        "input_sets": nsets,
+    }
+    if kind == "chunked":
+        res["tflops_f153"] = round(B * H * N * (4 * feature_dim(d) * dv + (chunk + 1) * (d + dv)) / sec / 1e12, 3)
+    del calls
+    torch_empty_cache()
+    return res
+
+
+def torch_empty_cache():
+    import torch
+
+    torch.cuda.empty_cache()
+
+
+def cpu_baseline(sample_heads):
+    """The oracle's restatement of the reference PyTorch path (kernels/pytorch_attention.py:27-42,
+    computed in bf16 as the reference does) on ``sample_heads`` heads of the headline workload,
+    timed on this host's cores; reported as TFLOP/s of the same algorithmic count."""
+    import torch
+
+    from oracle import reference as ref
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    _, _, B, H, N, d, dv, dt, seed, _, _, prescale = HEADLINE
+    q, k, v = make_inputs(1, sample_heads, N, d, dv, dt, seed, prescale, "cpu")
+    t0 = time.perf_counter()
+    ref.ref_based_attn(q, k, v)
+    sec = time.perf_counter() - t0
+    flop = sample_heads * N * (N + 1) / 2 * 2 * (d + dv)
+    return {
+        "value": round(flop / sec / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{sample_heads} of {B * H} heads at N={N} d={d} dv={dv}, restated reference ref_based_attn "
+                  f"(kernels/pytorch_attention.py:27-42) in bf16 on CPU, one pass, {sec:.2f} s "
+                  f"(extrapolated full-job time {sec * B * H / sample_heads:.1f} s)",
+        "sample_seconds": round(sec, 3),
+    }
+
+
+def load_traffic(kernel):
+    path = os.path.join(ROOT, "profiles", f"traffic_{kernel}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the multi-GPU sharding is described in "
+              "DESIGN.md and not launched", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+
+    head = measure(HEADLINE, args.steps, args.warmup, args.rotate, device)
+    per_config = {}
+    if args.configs == "all":
+        for cfg in CONFIGS:
+            try:
+                per_config[cfg[0]] = measure(cfg, args.steps, args.warmup, args.rotate, device)
+            except RuntimeError as e:
+                per_config[cfg[0]] = {"error": str(e)}
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_sample_heads)
+
+    achieved = head["tflops"]
+    line = {
+        "metric": METRIC,
+        "value": achieved,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "based_parallel_fwd causal B2 H16 N8192 d16 dv64 bf16 in/out, fp32 accumulate",
+                   "global_batch": 2, "heads": 16, "seq_len": 8192, "d": 16, "dv": 64, "parallelism": "single-gpu"},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic("based_parallel")},
+        "cpu_baseline": cpu,
+        "per_config": per_config,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

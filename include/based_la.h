@@ -1,0 +1,114 @@
+/*
+ * based_la.h -- C ABI of the MI355X (gfx950) BASED linear-attention library (libbased_la.so).
+ *
+ * Plain C: device pointers, sizes and a HIP stream handle, no C++ or torch types.  Every
+ * tensor is a contiguous row-major (B, H, N, .) array in device memory owned by the caller;
+ * the library allocates nothing per call.  Launches are asynchronous on the given stream
+ * (NULL = the default stream); the caller synchronises.
+ *
+ * Return value: 0 on success; a negative LA_ERR_* code for an argument error detected on the
+ * host before anything is launched; a positive value is a hipError_t reported by the runtime
+ * right after the launch.  la_status_string() turns either into text.  Nothing throws.
+ *
+ * The entry points replace the reference's Python-level kernel wrappers
+ * (Willy-Chan/trainium-linear-attention); each declaration names the function it stands in for.
+ */
+#ifndef BASED_LA_H
+#define BASED_LA_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LA_ABI_VERSION 1
+
+/* element types */
+#define LA_F32 0
+#define LA_BF16 1
+
+/* argument errors (negative) */
+#define LA_OK 0
+#define LA_ERR_NULL_POINTER (-1)
+#define LA_ERR_BAD_SHAPE (-2)
+#define LA_ERR_BAD_DTYPE (-3)
+#define LA_ERR_BAD_SCALAR (-4)
+#define LA_ERR_UNSUPPORTED_DIM (-5)
+#define LA_ERR_WORKSPACE (-6)
+#define LA_ERR_NO_DEVICE (-7)
+#define LA_ERR_BAD_ALIGNMENT (-8)
+
+/* Version of this ABI (LA_ABI_VERSION). */
+int la_abi_version(void);
+
+/* Static text for a status code returned by any la_* function. */
+const char* la_status_string(int status);
+
+/*
+ * Fused causal BASED attention, parallel (quadratic) form.
+ *
+ * Replaces solution_nki / the NKI parallel kernel: kernels/pytorch_attention.py:44-78 and
+ * kernels/nki_attention.py:25-115 (num and den accumulated per query block, out = num/(den+eps)).
+ *
+ *   s_tu = scale * q_t.k_u,  p = 1 + s + s^2/2,  den_t = sum_{u<=t} p_tu,
+ *   num_t = sum_{u<=t} p_tu v_u,  out_t = normalize ? num_t / (den_t + eps) : num_t.
+ *
+ * q, k: (B,H,N,d); v, out: (B,H,N,dv); in_dtype / out_dtype: LA_BF16 or LA_F32 (q, k and v
+ * share in_dtype).  den_or_null: optional (B,H,N) fp32 output of den_t (without eps).
+ * Limits: 1 <= d <= 128, 1 <= dv <= 128, scale > 0 and finite, eps >= 0 and finite.
+ * The reference passes scale = 1/sqrt(d) and eps = 1e-6.
+ */
+int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dtype,
+                          void* out, int out_dtype, float* den_or_null,
+                          int B, int H, int N, int d, int dv,
+                          float scale, float eps, int normalize, void* hip_stream);
+
+/*
+ * Chunked recurrent BASED attention (linear in N).
+ *
+ * Replaces chunked_nki_numerator / the NKI chunked kernel:
+ * benchmarks/chunked_attention_benchmark.py:96-126 and kernels/nki_attention_chunked.py:20-113.
+ * The feature map phi (benchmarks/chunked_attention_benchmark.py:34-53, dimension
+ * F = 1 + d + d(d+1)/2) is applied inside the kernel; the (F x dv) state and the F-long K-sum
+ * stay on chip across chunks.  normalize = 0 returns the numerator only (what the reference's
+ * chunked kernel returns); normalize = 1 divides by phi(q).z + eps like the parallel path.
+ * state_out_or_null: optional fp32 output of the final state per head, (B,H,F,dv+1) with the
+ * K-sum in the last column.  workspace: device scratch of at least
+ * la_based_chunked_workspace_bytes(...) bytes (may be NULL when that is 0).
+ * Limits: d == 16, 1 <= dv <= 64, chunk in {16, 32, 64, 128, 256}.
+ */
+size_t la_based_chunked_workspace_bytes(int B, int H, int N, int d, int dv, int chunk);
+int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dtype,
+                         void* out, int out_dtype, int B, int H, int N, int d, int dv, int chunk,
+                         float scale, float eps, int normalize,
+                         void* workspace, size_t workspace_bytes, float* state_out_or_null,
+                         void* hip_stream);
+
+/*
+ * Causal sliding-window softmax attention.
+ *
+ * Replaces nki_sliding_window_attn / the NKI sliding kernel:
+ * benchmarks/sliding_attention_benchmark.py:59-99 and kernels/nki_attention_sliding.py:30-132
+ * (valid keys t-W+1 <= u <= t, softmax of scale*q.k, times V).  Any window >= 1.
+ * q, k: (B,H,N,d); v, out: (B,H,N,dv).  Limits: 1 <= d <= 128, 1 <= dv <= 128.
+ */
+int la_sliding_window_fwd(const void* q, const void* k, const void* v, int in_dtype,
+                          void* out, int out_dtype, int B, int H, int N, int d, int dv,
+                          int window, float scale, void* hip_stream);
+
+/*
+ * BASED Taylor feature map, phi(x) = [1, x/d^(1/4), x_i^2/(sqrt(d) sqrt(2)),
+ * x_i x_j/sqrt(d) (i<j, row-major upper-triangle order)], rows x (rows, d) -> (rows, F).
+ *
+ * Replaces taylor_feature_map: benchmarks/chunked_attention_benchmark.py:23-53.
+ * Limits: 1 <= d <= 128.
+ */
+int la_taylor_feature_map(const void* x, int in_dtype, void* out, int out_dtype,
+                          long long rows, int d, void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BASED_LA_H */

@@ -1,0 +1,131 @@
+"""CPU checks of the C ABI: the library loads, exports every entry point include/based_la.h
+declares, and rejects bad arguments on the host before any launch (no GPU needed)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "based_la.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(la_\w+)\s*\(", text, re.M)))
+
+
+def _lib():
+    from kernels import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libbased_la.so not built")
+    return _lib.lib()
+
+
+def test_header_declares_expected_entry_points():
+    assert _declared() == sorted([
+        "la_abi_version", "la_status_string", "la_based_parallel_fwd", "la_based_chunked_workspace_bytes",
+        "la_based_chunked_fwd", "la_sliding_window_fwd", "la_taylor_feature_map"])
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_status_strings():
+    lib = _lib()
+    assert lib.la_abi_version() == 1
+    for code in range(-8, 1):
+        s = lib.la_status_string(code).decode()
+        assert s and s != "unknown status"
+
+
+def _codes():
+    from kernels import _lib
+    return _lib
+
+
+P = ctypes.c_void_p(16)   # dummy non-null, 16-byte aligned pointer; never dereferenced on error paths
+
+
+def test_parallel_argument_errors():
+    lib = _lib()
+    f = lib.la_based_parallel_fwd
+    ok_args = dict(q=P, k=P, v=P, dt=1, out=P, odt=1, den=None, B=1, H=1, N=8, d=16, dv=64, scale=0.25, eps=1e-6,
+                   norm=1)
+
+    def call(**kw):
+        a = dict(ok_args, **kw)
+        return f(a["q"], a["k"], a["v"], a["dt"], a["out"], a["odt"], a["den"], a["B"], a["H"], a["N"], a["d"],
+                 a["dv"], a["scale"], a["eps"], a["norm"], None)
+
+    assert call(q=None) == -1
+    assert call(d=0) == -2
+    assert call(N=-1) == -2
+    assert call(dt=7) == -3
+    assert call(odt=2) == -3
+    assert call(scale=0.0) == -4
+    assert call(scale=float("nan")) == -4
+    assert call(eps=-1.0) == -4
+    assert call(d=129) == -5
+    assert call(dv=200) == -5
+    assert call(q=ctypes.c_void_p(17)) == -8
+    assert call(N=0) == 0          # empty: nothing to launch
+    assert call(B=0) == 0
+
+
+def test_sliding_argument_errors():
+    lib = _lib()
+    f = lib.la_sliding_window_fwd
+
+    def call(q=P, W=64, scale=0.125, d=64, dv=64, N=8, dt=1):
+        return f(q, P, P, dt, P, 1, 1, 1, N, d, dv, W, scale, None)
+
+    assert call(q=None) == -1
+    assert call(W=0) == -4
+    assert call(scale=-1.0) == -4
+    assert call(d=0) == -2
+    assert call(dt=3) == -3
+    assert call(d=256) == -5
+    assert call(N=0) == 0
+
+
+def test_chunked_argument_errors():
+    lib = _lib()
+    f = lib.la_based_chunked_fwd
+
+    def call(q=P, chunk=64, d=16, dv=64, N=8, ws=P, wsb=1 << 30, scale=0.25, eps=1e-6):
+        return f(q, P, P, 1, P, 1, 1, 1, N, d, dv, chunk, scale, eps, 0, ws, wsb, None, None)
+
+    assert call(q=None) == -1
+    assert call(chunk=0) == -2
+    assert call(scale=0.0) == -4
+    assert call(N=0) == 0
+
+
+def test_feature_map_argument_errors():
+    lib = _lib()
+    f = lib.la_taylor_feature_map
+    assert f(None, 0, P, 0, 4, 16, None) == -1
+    assert f(P, 0, P, 0, -1, 16, None) == -2
+    assert f(P, 0, P, 0, 4, 0, None) == -2
+    assert f(P, 5, P, 0, 4, 16, None) == -3
+    assert f(P, 0, P, 0, 4, 200, None) == -5
+    assert f(P, 0, P, 0, 0, 16, None) == 0
+
+
+def test_python_wrappers_refuse_cpu_tensors():
+    import torch
+    import kernels
+    q = torch.zeros(1, 1, 4, 16)
+    with pytest.raises(RuntimeError):
+        kernels.solution_nki(q, q, q)
+    with pytest.raises(RuntimeError):
+        kernels.nki_sliding_window_attn(q, q, q)
+    with pytest.raises(RuntimeError):
+        kernels.chunked_nki_numerator(q, q, q)
+    with pytest.raises(RuntimeError):
+        kernels.taylor_feature_map(q)

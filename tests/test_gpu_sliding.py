@@ -1,0 +1,78 @@
+"""GPU parity of the sliding-window softmax kernel (la_sliding_window_fwd) against the oracle."""
+
+import pytest
+import torch
+
+from oracle import reference as ref
+from tests.helpers import err, load_golden, rand_qkv, to_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16 = 2e-2
+TOL_F32 = 1e-4
+
+
+def _kernels():
+    import kernels
+    return kernels
+
+
+@pytest.mark.parametrize("name", ["sliding_b1h2n131d64w1", "sliding_b1h2n131d64w17", "sliding_b1h2n131d64w64"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_golden(name, dtype):
+    K = _kernels()
+    g = load_golden(name)
+    q, k, v = (torch.from_numpy(g[x]) for x in "qkv")
+    y = K.sliding_window_attn(*to_dev(q, k, v, dtype=dtype), window_size=int(g["window"]), out_dtype=torch.float32)
+    e = err(y, torch.from_numpy(g["y"]))
+    print(f"{name} {dtype} err={e:.3e}")
+    assert e < (TOL_BF16 if dtype == torch.bfloat16 else TOL_F32)
+
+
+@pytest.mark.parametrize("W", [1, 2, 31, 32, 33, 63, 64, 65, 100, 128, 129, 300, 5000])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_windows(W, dtype):
+    K = _kernels()
+    q, k, v = rand_qkv(1, 2, 517, 64, 64, seed=W, dtype=dtype)
+    y = K.sliding_window_attn(*to_dev(q, k, v), window_size=W, out_dtype=torch.float32)
+    want = ref.sliding_dense(q, k, v, window_size=W)
+    e = err(y, want)
+    print(f"W={W} {dtype} err={e:.3e}")
+    assert e < (TOL_BF16 if dtype == torch.bfloat16 else TOL_F32)
+
+
+@pytest.mark.parametrize("d,dv", [(16, 16), (32, 64), (64, 32), (128, 128), (8, 24), (40, 72)])
+def test_head_dims(d, dv):
+    K = _kernels()
+    q, k, v = rand_qkv(2, 1, 300, d, dv, seed=d + dv, dtype=torch.bfloat16)
+    y = K.sliding_window_attn(*to_dev(q, k, v), window_size=50, out_dtype=torch.float32)
+    want = ref.sliding_dense(q, k, v, window_size=50)
+    assert err(y, want) < TOL_BF16
+
+
+def test_window_one_is_identity():
+    K = _kernels()
+    q, k, v = to_dev(*rand_qkv(1, 2, 130, 64, 64, seed=1, dtype=torch.bfloat16))
+    y = K.nki_sliding_window_attn(q, k, v, window_size=1)
+    assert torch.equal(y, v)
+
+
+def test_full_window_is_causal_sdpa():
+    K = _kernels()
+    q, k, v = rand_qkv(1, 2, 200, 64, 64, seed=5, dtype=torch.float32)
+    y = K.nki_sliding_window_attn(*to_dev(q, k, v), window_size=10_000)
+    want = torch.nn.functional.scaled_dot_product_attention(q.double(), k.double(), v.double(), is_causal=True)
+    assert err(y, want) < TOL_F32
+
+
+def test_config4_bf16():
+    K = _kernels()
+    cfg = ref.CONFIGS["c4_sliding_bf16"]
+    q, k, v = ref.config_inputs(cfg)
+    y = K.sliding_window_attn(*to_dev(q, k, v), window_size=cfg.window, out_dtype=torch.float32)
+    want = ref.sliding_banded(q, k, v, window_size=cfg.window, dtype=torch.float64)
+    e = err(y, want)
+    print(f"config4 err={e:.3e}")
+    assert e < TOL_BF16
+    y16 = K.nki_sliding_window_attn(*to_dev(q, k, v), window_size=cfg.window)
+    assert y16.dtype == torch.bfloat16 and torch.equal(y16, y.to(torch.bfloat16))

@@ -1,0 +1,166 @@
+// C-ABI entry points of libbased_la.so (declared in include/based_la.h).
+//
+// Host-side validation happens here, before any launch; argument errors return negative
+// LA_ERR_* codes and launch/runtime errors return the positive hipError_t.  Nothing throws
+// and nothing is allocated.
+#include <math.h>
+
+#include "../../include/based_la.h"
+#include "la_internal.hpp"
+
+namespace {
+
+bool dtype_ok(int t) { return t == LA_F32 || t == LA_BF16; }
+bool finite_f(float x) { return isfinite(x) != 0; }
+
+int check_common(const void* q, const void* k, const void* v, const void* out, int in_dtype, int out_dtype,
+                 int B, int H, int N, int d, int dv) {
+  if (B < 0 || H < 0 || N < 0 || d < 1 || dv < 1) return LA_ERR_BAD_SHAPE;
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return LA_ERR_BAD_DTYPE;
+  if ((long long)B * H * N == 0) return LA_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr) return LA_ERR_NULL_POINTER;
+  if ((long long)B * H > 0x7fffffffLL || (long long)N * (d > dv ? d : dv) > 0x7fffffffLL) return LA_ERR_BAD_SHAPE;
+  const size_t esz = in_dtype == LA_F32 ? 4 : 2;
+  const uintptr_t mask = esz - 1;
+  if ((reinterpret_cast<uintptr_t>(q) & mask) || (reinterpret_cast<uintptr_t>(k) & mask) ||
+      (reinterpret_cast<uintptr_t>(v) & mask))
+    return LA_ERR_BAD_ALIGNMENT;
+  const uintptr_t omask = (out_dtype == LA_F32 ? 4 : 2) - 1;
+  if (reinterpret_cast<uintptr_t>(out) & omask) return LA_ERR_BAD_ALIGNMENT;
+  return LA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int la_abi_version(void) { return LA_ABI_VERSION; }
+
+const char* la_status_string(int status) {
+  switch (status) {
+    case LA_OK: return "success";
+    case LA_ERR_NULL_POINTER: return "null tensor pointer";
+    case LA_ERR_BAD_SHAPE: return "invalid shape (negative size, d or dv < 1, or a size beyond the 32-bit index range)";
+    case LA_ERR_BAD_DTYPE: return "unsupported dtype (expected LA_F32 or LA_BF16)";
+    case LA_ERR_BAD_SCALAR: return "invalid scalar argument (scale must be finite and > 0, eps finite and >= 0, window >= 1)";
+    case LA_ERR_UNSUPPORTED_DIM: return "unsupported head / value dimension or chunk size for this kernel";
+    case LA_ERR_WORKSPACE: return "workspace too small";
+    case LA_ERR_NO_DEVICE: return "no HIP device";
+    case LA_ERR_BAD_ALIGNMENT: return "tensor pointer not aligned to its element size";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
+  return "unknown status";
+}
+
+int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype,
+                          float* den_or_null, int B, int H, int N, int d, int dv, float scale, float eps,
+                          int normalize, void* hip_stream) {
+  int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
+  if (rc != LA_OK) return rc;
+  if (d > 128 || dv > 128) return LA_ERR_UNSUPPORTED_DIM;
+  if (!finite_f(scale) || !(scale > 0.f) || !finite_f(eps) || eps < 0.f) return LA_ERR_BAD_SCALAR;
+  if ((long long)B * H * N == 0) return LA_OK;
+  if (den_or_null != nullptr && (reinterpret_cast<uintptr_t>(den_or_null) & 3)) return LA_ERR_BAD_ALIGNMENT;
+  la::ParallelArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.den = den_or_null;
+  a.BH = B * H;
+  a.N = N;
+  a.d = d;
+  a.dv = dv;
+  a.scale = scale;
+  a.eps = eps;
+  a.normalize = normalize != 0;
+  a.in_f32 = in_dtype == LA_F32;
+  a.out_f32 = out_dtype == LA_F32;
+  return la::launch_based_parallel(a, static_cast<hipStream_t>(hip_stream));
+}
+
+size_t la_based_chunked_workspace_bytes(int B, int H, int N, int d, int dv, int chunk) {
+  if (B < 1 || H < 1 || N < 1 || d < 1 || dv < 1 || chunk < 1) return 0;
+  return la::chunked_workspace_bytes(B * H, N, d, dv, chunk);
+}
+
+int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
+                         int H, int N, int d, int dv, int chunk, float scale, float eps, int normalize,
+                         void* workspace, size_t workspace_bytes, float* state_out_or_null, void* hip_stream) {
+  int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
+  if (rc != LA_OK) return rc;
+  if (!finite_f(scale) || !(scale > 0.f) || !finite_f(eps) || eps < 0.f) return LA_ERR_BAD_SCALAR;
+  if (chunk < 1) return LA_ERR_BAD_SHAPE;
+  if ((long long)B * H * N == 0) return LA_OK;
+  const size_t need = la::chunked_workspace_bytes(B * H, N, d, dv, chunk);
+  if (need == (size_t)-1) return LA_ERR_UNSUPPORTED_DIM;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
+  if (state_out_or_null != nullptr && (reinterpret_cast<uintptr_t>(state_out_or_null) & 3)) return LA_ERR_BAD_ALIGNMENT;
+  la::ChunkedArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.state_out = state_out_or_null;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  a.BH = B * H;
+  a.N = N;
+  a.d = d;
+  a.dv = dv;
+  a.chunk = chunk;
+  a.scale = scale;
+  a.eps = eps;
+  a.normalize = normalize != 0;
+  a.in_f32 = in_dtype == LA_F32;
+  a.out_f32 = out_dtype == LA_F32;
+  return la::launch_based_chunked(a, static_cast<hipStream_t>(hip_stream));
+}
+
+int la_sliding_window_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
+                          int H, int N, int d, int dv, int window, float scale, void* hip_stream) {
+  int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
+  if (rc != LA_OK) return rc;
+  if (d > 128 || dv > 128) return LA_ERR_UNSUPPORTED_DIM;
+  if (window < 1 || !finite_f(scale) || !(scale > 0.f)) return LA_ERR_BAD_SCALAR;
+  if ((long long)B * H * N == 0) return LA_OK;
+  la::SlidingArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.BH = B * H;
+  a.N = N;
+  a.d = d;
+  a.dv = dv;
+  a.window = window;
+  a.scale = scale;
+  a.in_f32 = in_dtype == LA_F32;
+  a.out_f32 = out_dtype == LA_F32;
+  return la::launch_sliding_window(a, static_cast<hipStream_t>(hip_stream));
+}
+
+int la_taylor_feature_map(const void* x, int in_dtype, void* out, int out_dtype, long long rows, int d,
+                          void* hip_stream) {
+  if (rows < 0 || d < 1) return LA_ERR_BAD_SHAPE;
+  if (d > 128) return LA_ERR_UNSUPPORTED_DIM;
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return LA_ERR_BAD_DTYPE;
+  if (rows == 0) return LA_OK;
+  if (x == nullptr || out == nullptr) return LA_ERR_NULL_POINTER;
+  if ((reinterpret_cast<uintptr_t>(x) & (in_dtype == LA_F32 ? 3 : 1)) ||
+      (reinterpret_cast<uintptr_t>(out) & (out_dtype == LA_F32 ? 3 : 1)))
+    return LA_ERR_BAD_ALIGNMENT;
+  const long long F = 1 + (long long)d + (long long)d * (d + 1) / 2;
+  if (rows * F > (1LL << 40)) return LA_ERR_BAD_SHAPE;
+  la::FeatureMapArgs a{};
+  a.x = x;
+  a.out = out;
+  a.rows = rows;
+  a.d = d;
+  a.in_f32 = in_dtype == LA_F32;
+  a.out_f32 = out_dtype == LA_F32;
+  return la::launch_feature_map(a, static_cast<hipStream_t>(hip_stream));
+}
+
+}  // extern "C"

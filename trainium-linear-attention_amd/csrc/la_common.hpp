@@ -1,0 +1,69 @@
+// Shared device helpers for the gfx950 BASED kernels: vector types, bf16 packing, MFMA
+// wrappers and the 32x32 accumulator layout.
+//
+// MFMA layout used throughout (v_mfma_f32_32x32x16_bf16, wave64):
+//   A (32 x 16): lane l holds row l%32, k = 8*(l/32) .. +7
+//   B (16 x 32): lane l holds col l%32, k = 8*(l/32) .. +7
+//   C (32 x 32): lane l holds col l%32, rows 8*(i/4) + 4*(l/32) + (i%4) for i = 0..15
+// Only the pairing "element e of lane group h in A with element e of lane group h in B" is
+// relied on for the contraction index, so any K permutation applied to both operands is fine.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace la {
+
+typedef uint32_t u32;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(u32)))) u32 u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(u32)))) u32 u32x2;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// float -> bf16 bits, round to nearest even (the hardware conversion on gfx950).
+__device__ __forceinline__ u32 pack_bf16x2(float lo, float hi) {
+  bf16x2 p = __builtin_convertvector((f32x2){lo, hi}, bf16x2);
+  return __builtin_bit_cast(u32, p);
+}
+
+__device__ __forceinline__ float bf16_lo_to_f32(u32 w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi_to_f32(u32 w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, (u32)b << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  return (uint16_t)(pack_bf16x2(f, 0.f) & 0xffffu);
+}
+
+// sum += a.lo*b.lo + a.hi*b.hi over packed bf16 pairs, fp32 accumulate (v_dot2c_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(u32 a, u32 b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), acc,
+                                         false);
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 splat16(float x) {
+  f32x16 r;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r[i] = x;
+  return r;
+}
+
+// Row (key / dv index) of element i of a 32x32 accumulator held by lane group h.
+__device__ __forceinline__ int c32_row(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
+
+}  // namespace la

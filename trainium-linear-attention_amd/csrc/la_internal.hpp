@@ -1,0 +1,80 @@
+// Host-side launch descriptors shared between the C-ABI layer (capi.hip) and the kernel
+// translation units.  Internal to libbased_la.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace la {
+
+struct ParallelArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  float* den;          // optional, (BH, N) fp32, den without eps
+  int BH, N, d, dv;
+  float scale, eps;
+  bool normalize;
+  bool in_f32, out_f32;
+};
+
+struct SlidingArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int BH, N, d, dv, window;
+  float scale;
+  bool in_f32, out_f32;
+};
+
+struct ChunkedArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  float* state_out;    // optional, (BH, F, dv + 1) fp32
+  void* workspace;
+  size_t workspace_bytes;
+  int BH, N, d, dv, chunk;
+  float scale, eps;
+  bool normalize;
+  bool in_f32, out_f32;
+};
+
+struct FeatureMapArgs {
+  const void* x;
+  void* out;
+  long long rows;
+  int d;
+  bool in_f32, out_f32;
+};
+
+// Each launcher validates what only it knows (supported tile shapes), launches on `stream`
+// and returns 0, a negative LA_ERR_* code, or a positive hipError_t.
+int launch_based_parallel(const ParallelArgs& a, hipStream_t stream);
+int launch_sliding_window(const SlidingArgs& a, hipStream_t stream);
+size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk);
+int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream);
+int launch_feature_map(const FeatureMapArgs& a, hipStream_t stream);
+
+// Work-group order for causal query blocks: heaviest (last) blocks first, and -- when the
+// head count is a multiple of the 8 XCDs -- every XCD works through whole heads in turn so a
+// head's K/V prefix stays in that XCD's L2.  Work-groups are dispatched to XCDs round-robin
+// by work-group id.
+__device__ __forceinline__ void map_causal_block(int wg, int BH, int nqb, int& bh, int& qb) {
+  if ((BH & 7) == 0) {
+    const int x = wg & 7, slot = wg >> 3;
+    const int hx = slot / nqb;
+    qb = nqb - 1 - (slot - hx * nqb);
+    bh = hx * 8 + x;
+  } else {
+    const int r = wg / BH;
+    qb = nqb - 1 - r;
+    bh = wg - r * BH;
+  }
+}
+
+}  // namespace la

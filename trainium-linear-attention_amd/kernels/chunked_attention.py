@@ -1,0 +1,88 @@
+"""Chunked recurrent BASED attention and the Taylor feature map on MI355X -- drop-in for the
+reference's ``taylor_feature_map`` and ``chunked_nki_numerator``
+(benchmarks/chunked_attention_benchmark.py:34-53, :96-126).
+
+* ``taylor_feature_map(x)`` -- phi(x) = [1, x/d^(1/4), x_i^2/(sqrt(d) sqrt(2)), x_i x_j/sqrt(d)]
+  (i < j in triu order), computed by a HIP kernel; returns x.dtype.
+* ``chunked_nki_numerator(q, k, v, chunk_size=64)`` -- numerator only, as the NKI kernel
+  returns (kernels/nki_attention_chunked.py:56).
+* ``chunked_based_attn(q, k, v, chunk_size=64, eps=1e-6)`` -- the same recurrence carrying the
+  K-sum so it also normalises; equal to ``solution_nki`` up to rounding.
+
+The feature map is applied inside the chunked kernel: phi(Q), phi(K) never reach HBM, and the
+state stays on chip across chunks (the NKI kernel round-trips it through HBM,
+kernels/nki_attention_chunked.py:92-102).  dv may differ from d.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .pytorch_attention import _as_kernel_input, _check_qkv, _compute_dtype
+
+__all__ = ["taylor_feature_map", "feature_dim", "chunked_nki_numerator", "chunked_based_attn", "based_chunked"]
+
+
+def feature_dim(d: int) -> int:
+    return 1 + d + d * (d + 1) // 2
+
+
+def taylor_feature_map(x):
+    """phi(x) for x of shape (..., d); output (..., 1 + d + d(d+1)/2) in x.dtype."""
+    _lib.require_gpu(x)
+    d = x.shape[-1]
+    cdt = _compute_dtype(x.dtype)
+    kdt = x.dtype if x.dtype in (torch.float32, torch.bfloat16) else torch.float32
+    xc = _as_kernel_input(x, cdt)
+    rows = xc.numel() // d if d > 0 else 0
+    out = torch.empty(*x.shape[:-1], feature_dim(d), dtype=kdt, device=x.device)
+    rc = _lib.lib().la_taylor_feature_map(_lib.ptr(xc), _lib.dtype_code(cdt), _lib.ptr(out), _lib.dtype_code(kdt),
+                                          rows, d, _lib.stream_of(x))
+    _lib.check(rc, "la_taylor_feature_map")
+    return out if out.dtype == x.dtype else out.to(x.dtype)
+
+
+def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, out_dtype=None,
+                  return_state=False):
+    """Chunked recurrent BASED attention through ``la_based_chunked_fwd``.
+
+    ``return_state`` also returns the final per-head state in the reference feature basis:
+    (b, h, F, dv + 1) fp32 = [sum_u phi(k_u) v_u^T | sum_u phi(k_u)].
+    """
+    _check_qkv(q, k, v)
+    b, h, t, d = q.shape
+    dv = v.shape[-1]
+    cdt = _compute_dtype(q.dtype)
+    odt = q.dtype if out_dtype is None else out_dtype
+    kdt = odt if odt in (torch.float32, torch.bfloat16) else torch.float32
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    qc, kc, vc = (_as_kernel_input(x, cdt) for x in (q, k, v))
+    out = torch.empty(b, h, t, dv, dtype=kdt, device=q.device)
+    L = _lib.lib()
+    ws_bytes = int(L.la_based_chunked_workspace_bytes(b, h, t, d, dv, int(chunk_size)))
+    if ws_bytes == (1 << 64) - 1:
+        raise _lib.BasedLAError(f"chunked kernel does not support d={d}, dv={dv}, chunk={chunk_size}")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    state = torch.empty(b, h, feature_dim(d), dv + 1, dtype=torch.float32, device=q.device) if return_state else None
+    rc = L.la_based_chunked_fwd(
+        _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.dtype_code(cdt), _lib.ptr(out), _lib.dtype_code(kdt),
+        b, h, t, d, dv, int(chunk_size), float(scale), float(eps), 1 if normalize else 0,
+        _lib.ptr(ws), ws_bytes, _lib.ptr(state), _lib.stream_of(q))
+    _lib.check(rc, "la_based_chunked_fwd")
+    if out.dtype != odt:
+        out = out.to(odt)
+    return (out, state) if return_state else out
+
+
+def chunked_nki_numerator(q, k, v, chunk_size=64):
+    """Numerator-only chunked BASED attention (reference signature); returns q.dtype."""
+    return based_chunked(q, k, v, chunk_size=chunk_size, normalize=False)
+
+
+def chunked_based_attn(q, k, v, chunk_size=64, eps=1e-6):
+    """Normalised chunked BASED attention; returns q.dtype."""
+    return based_chunked(q, k, v, chunk_size=chunk_size, eps=eps, normalize=True)
