@@ -1,8 +1,704 @@
-// Chunked recurrent BASED attention (kernel under construction).
+// Chunked recurrent BASED attention for gfx950 (d = 16, dv <= 64).
+//
+// Replaces the NKI chunked kernel (kernels/nki_attention_chunked.py:27-113) and the feature
+// map + padding of its wrapper (benchmarks/chunked_attention_benchmark.py:96-126).  The
+// recurrence is the reference's: per chunk c of 64 tokens,
+//     out_c = phi(Q_c) S + causal(phi(Q_c) phi(K_c)^T) V_c,    S += phi(K_c)^T V_c,
+// extended with the K-sum z (den = phi(q).z + intra row sum) so it can also normalise.
+//
+// Design for MI355X:
+//   * phi is never materialised in HBM.  The Taylor features of q and k are formed in
+//     registers right before the MFMAs that consume them, from q~ = sqrt(c) q, k~ = sqrt(c) k.
+//   * Internal feature basis (160 features + the constant): 10 "slots" of 16,
+//       slot 0: q~_i (linear)          slot 1: q~_i^2 / 2 (q side) | k~_i^2 (k side)
+//       slot 2j, 2j+1 (j = 1..4): q~_i q~_{i+delta} (i + delta mod 16), delta = j and j + 4;
+//       delta = 8 visits every pair twice, so its k side carries a factor 1/2.
+//     With it, phi(q).phi(k) = 1 + s + s^2/2 exactly, and in every K-step of the
+//     phi(Q).S MFMA the lane groups that hold different slots run the same instructions on
+//     rotated copies of q~ (register indices are compile-time constants).
+//   * The constant feature is exact fp32: S_0 = sum v and z_0 = token count.
+//   * phi operands and the state operand are fp16 (the state itself accumulates in fp32 MFMA
+//     accumulators); q~ and k~ carry 2^(+-sigma/2) so the state stays well inside the fp16
+//     range for long sequences.  Intra-chunk terms use the d-form (q.k) exactly like the
+//     diagonal block of the parallel kernel (fp16 P, exact "1" through a mask MFMA).
+//   * Sequence parallelism: the sequence is cut into P segments.  Kernel 1 computes each
+//     segment's state increment (fp16 S, fp32 z and sum v) into the workspace; kernel 2 runs
+//     the chunk recurrence of every segment in parallel, starting from the sum of the
+//     increments of the earlier segments.  Within a work-group (4 waves) the state lives in
+//     registers: wave w owns slots {w, w+4, w+8} for all dv, and shares them with the other
+//     waves through LDS (fp16) once per chunk.
+#include <math.h>
+
 #include "../../include/based_la.h"
+#include "la_common.hpp"
 #include "la_internal.hpp"
 
 namespace la {
-size_t chunked_workspace_bytes(int, int, int, int, int) { return (size_t)-1; }
-int launch_based_chunked(const ChunkedArgs&, hipStream_t) { return LA_ERR_UNSUPPORTED_DIM; }
+
+namespace {
+
+constexpr int CH = 64;          // tokens per chunk
+constexpr int NF = 160;         // internal features without the constant
+constexpr int NSLOT = 10;
+constexpr int DVC = 64;         // dv padded
+constexpr int STS = NF + 8;     // LDS row stride of S^T (fp16): 84 dwords, conflict-free 16 B reads
+constexpr int KTS = CH + 4;     // LDS row stride of k~^T (fp32)
+constexpr int VTS = CH + 8;     // LDS row stride of V^T (fp16): 16 B aligned rows
+constexpr int QKS = 16 + 8;     // LDS row stride of Q, K (bf16)
+
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f4;
+
+__device__ __forceinline__ f32x4 mfma16_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
+}
+__device__ __forceinline__ f32x4 mfma16_bf16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+
+struct ChunkParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  void* out;
+  float* state_out;
+  uint16_t* wsS;    // [BH][P][DVC][NF] fp16 segment increments of S (transposed, internal basis)
+  float* wsZ;       // [BH][P][NF]
+  float* wsV;       // [BH][P][DVC]  sum of v over the segment
+  int BH, N, dv, P, seg_chunks;
+  float inv_c, inv_c2, fscale, eps;   // intra d-form constants (as in the parallel kernel)
+  float qscale;                       // 2^-k on q for the intra scores
+  float qphi, kphi;                   // q~ = qphi * q, k~ = kphi * k
+  float W;                            // weight of "1" in intra u units; q-side phi carries it too
+  float st_lin, st_diag, st_off;      // internal -> reference feature basis factors (state export)
+  u32 ones_hi, ones_lo;
+  int normalize, out_f32, vec;
+};
+
+__device__ __forceinline__ void map_segment(int wg, int BH, int P, int& bh, int& p) {
+  if ((BH & 7) == 0) {
+    const int x = wg & 7, slot = wg >> 3;
+    const int hx = slot / P;
+    p = slot - hx * P;
+    bh = hx * 8 + x;
+  } else {
+    bh = wg / P;
+    p = wg - bh * P;
+  }
+}
+
+// Shared-memory image of one chunk.
+struct ChunkLds {
+  uint16_t Qs[CH * QKS];     // bf16 row-major
+  uint16_t Ks[CH * QKS];     // bf16 row-major
+  float KT[16 * KTS];        // k~^T fp32
+  uint16_t VT[DVC * VTS];    // V^T fp16
+  uint16_t ST[DVC * STS];    // S^T fp16 (internal basis, scaled by W on use)
+  float Z[NF];               // z (internal basis) fp32
+  float S0[DVC];             // sum of v over all earlier tokens, fp32
+  float S0c[DVC];            // sum of v over this chunk
+};
+
+// Registers that carry one chunk from global memory to LDS.
+struct ChunkRegs {
+  u32x4 qk;          // threads 0..127: q rows, 128..255: k rows (16 B each)
+  u32x2 v[4];        // 4 tokens x 4 dv of V
+};
+
+template <bool VEC>
+__device__ __forceinline__ void chunk_load(ChunkRegs& r, const ChunkParams& p, const uint16_t* qg, const uint16_t* kg,
+                                           const uint16_t* vg, int row0, int tid) {
+  const int N = p.N, dv = p.dv;
+  {
+    const int t = tid & 127, row = row0 + (t >> 1), col = 8 * (t & 1);
+    const uint16_t* base = (tid < 128) ? qg : kg;
+    u32x4 x = {0u, 0u, 0u, 0u};
+    if (row < N) {
+      const uint16_t* src = base + (size_t)row * 16 + col;
+      if (VEC) {
+        x = *reinterpret_cast<const u32x4*>(src);
+      } else {
+        uint16_t e[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = src[i];
+        x = (u32x4){e[0] | ((u32)e[1] << 16), e[2] | ((u32)e[3] << 16), e[4] | ((u32)e[5] << 16),
+                    e[6] | ((u32)e[7] << 16)};
+      }
+    }
+    r.qk = x;
+  }
+  {
+    const int g4 = tid & 15, kg4 = tid >> 4, col = 4 * g4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = row0 + 4 * kg4 + i;
+      u32x2 x = {0u, 0u};
+      if (row < N && col < dv) {
+        const uint16_t* src = vg + (size_t)row * dv + col;
+        if (VEC) {
+          x = *reinterpret_cast<const u32x2*>(src);
+        } else {
+          uint16_t e[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) e[t] = (col + t < dv) ? src[t] : (uint16_t)0;
+          x = (u32x2){e[0] | ((u32)e[1] << 16), e[2] | ((u32)e[3] << 16)};
+        }
+      }
+      r.v[i] = x;
+    }
+  }
+}
+
+__device__ __forceinline__ void chunk_store(const ChunkRegs& r, ChunkLds& L, float kphi, int tid) {
+  {
+    const int t = tid & 127, row = t >> 1, col = 8 * (t & 1);
+    if (tid < 128) {
+      *reinterpret_cast<u32x4*>(&L.Qs[row * QKS + col]) = r.qk;
+    } else {
+      *reinterpret_cast<u32x4*>(&L.Ks[row * QKS + col]) = r.qk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        L.KT[(col + 2 * e) * KTS + row] = kphi * bf16_lo_to_f32(r.qk[e]);
+        L.KT[(col + 2 * e + 1) * KTS + row] = kphi * bf16_hi_to_f32(r.qk[e]);
+      }
+    }
+  }
+  {
+    const int g4 = tid & 15, kg4 = tid >> 4;
+    const u32 a0 = r.v[0][0], a1 = r.v[1][0], a2 = r.v[2][0], a3 = r.v[3][0];
+    const u32 b0 = r.v[0][1], b1 = r.v[1][1], b2 = r.v[2][1], b3 = r.v[3][1];
+    const u32x2 c0 = {pack_f16x2(bf16_lo_to_f32(a0), bf16_lo_to_f32(a1)), pack_f16x2(bf16_lo_to_f32(a2), bf16_lo_to_f32(a3))};
+    const u32x2 c1 = {pack_f16x2(bf16_hi_to_f32(a0), bf16_hi_to_f32(a1)), pack_f16x2(bf16_hi_to_f32(a2), bf16_hi_to_f32(a3))};
+    const u32x2 c2 = {pack_f16x2(bf16_lo_to_f32(b0), bf16_lo_to_f32(b1)), pack_f16x2(bf16_lo_to_f32(b2), bf16_lo_to_f32(b3))};
+    const u32x2 c3 = {pack_f16x2(bf16_hi_to_f32(b0), bf16_hi_to_f32(b1)), pack_f16x2(bf16_hi_to_f32(b2), bf16_hi_to_f32(b3))};
+    uint16_t* dst = &L.VT[(4 * g4) * VTS + 4 * kg4];
+    *reinterpret_cast<u32x2*>(dst) = c0;
+    *reinterpret_cast<u32x2*>(dst + VTS) = c1;
+    *reinterpret_cast<u32x2*>(dst + 2 * VTS) = c2;
+    *reinterpret_cast<u32x2*>(dst + 3 * VTS) = c3;
+  }
+}
+
+// delta (pair offset) of a slot on the k side, and its extra factor
+__device__ __forceinline__ int slot_delta(int s) { return s < 2 ? 0 : ((s & 1) ? (s >> 1) + 4 : (s >> 1)); }
+
+// A fragment (16 features x 32 tokens) of phi(K)^T for slot s, K-step ks: lane (feature row
+// r = l%16, group g) holds phi_{s,r}(k_u) for tokens u = 32ks + 8g .. +7, as fp16.
+__device__ __forceinline__ u32x4 phi_k_frag(const ChunkLds& L, int s, int ks, int r, int g) {
+  const float* a = &L.KT[r * KTS + 32 * ks + 8 * g];
+  const f4 a0 = *reinterpret_cast<const f4*>(a), a1 = *reinterpret_cast<const f4*>(a + 4);
+  float x[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+  if (s == 0) {
+    // linear: k~_r
+  } else if (s == 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = x[e] * x[e];
+  } else {
+    const int dl = slot_delta(s);
+    const float* b = &L.KT[((r + dl) & 15) * KTS + 32 * ks + 8 * g];
+    const f4 b0 = *reinterpret_cast<const f4*>(b), b1 = *reinterpret_cast<const f4*>(b + 4);
+    const float y[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+    const float f = (dl == 8) ? 0.5f : 1.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = x[e] * (y[e] * f);
+  }
+  return (u32x4){pack_f16x2(x[0], x[1]), pack_f16x2(x[2], x[3]), pack_f16x2(x[4], x[5]), pack_f16x2(x[6], x[7])};
+}
+
+// State update for the slots a wave owns: S[slot][nt] += phi(K)^T V (all dv), z[slot] += sum
+// over tokens of phi(K).  S: accumulators (rows = features 4g+i, col = dv 16nt + l%16).
+template <int NS>
+__device__ __forceinline__ void update_slots(const ChunkLds& L, f32x4 (&S)[3][4], float (&z)[3], int w, int lane) {
+  const int r = lane & 15, g = lane >> 4;
+  constexpr u32 kOnes = 0x3c003c00u;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    u32x4 vb[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+      vb[nt] = *reinterpret_cast<const u32x4*>(&L.VT[(16 * nt + r) * VTS + 32 * ks + 8 * g]);
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int s = w + 4 * j;
+      const u32x4 a = phi_k_frag(L, s, ks, r, g);
+      float zz = z[j];
+      zz = dot2_f16(a[0], kOnes, zz);
+      zz = dot2_f16(a[1], kOnes, zz);
+      zz = dot2_f16(a[2], kOnes, zz);
+      zz = dot2_f16(a[3], kOnes, zz);
+      z[j] = zz;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) S[j][nt] = mfma16_f16(a, vb[nt], S[j][nt]);
+    }
+  }
+}
+
+// Column sums of V over this chunk (fp16 V exact, fp32 sums) into L.S0c; threads 0..255:
+// dv row tid/4, token quarter tid%4.
+__device__ __forceinline__ float chunk_vsum_part(const ChunkLds& L, int tid) {
+  constexpr u32 kOnes = 0x3c003c00u;
+  const uint16_t* src = &L.VT[(tid >> 2) * VTS + 16 * (tid & 3)];
+  const u32x4 a = *reinterpret_cast<const u32x4*>(src), b = *reinterpret_cast<const u32x4*>(src + 8);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s = dot2_f16(a[e], kOnes, s);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s = dot2_f16(b[e], kOnes, s);
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  return s;   // full chunk sum of dv row tid/4, in every lane of the quad
+}
+
+// Reduces a per-lane partial over the 4 lane groups (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float sum_groups(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+// Writes the wave's slots of S (fp16, transposed) and z into LDS.  z[j] holds per-lane partial
+// sums (row r = lane % 16, split over the 4 lane groups).
+template <int NS>
+__device__ __forceinline__ void publish_slots(ChunkLds& L, const f32x4 (&S)[3][4], const float (&z)[3], int w, int lane) {
+  const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const int s = w + 4 * j;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const u32x2 pk = {pack_f16x2(S[j][nt][0], S[j][nt][1]), pack_f16x2(S[j][nt][2], S[j][nt][3])};
+      *reinterpret_cast<u32x2*>(&L.ST[(16 * nt + r) * STS + 16 * s + 4 * g]) = pk;
+    }
+    const float zt = sum_groups(z[j]);
+    if (g == 0) L.Z[16 * s + r] = zt;
+  }
+}
+
+// -------------------------------------------------------------------------------------------
+// Kernel 1: per (head, segment < P-1) state increment of the segment.
+template <bool VEC>
+__global__ __launch_bounds__(256) void chunked_segment_kernel(const ChunkParams p) {
+  __shared__ __attribute__((aligned(16))) ChunkLds L;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int bh, seg;
+  map_segment(blockIdx.x, p.BH, p.P - 1, bh, seg);
+  const size_t hrow = (size_t)bh * p.N;
+  const uint16_t* qg = p.q + hrow * 16;
+  const uint16_t* kg = p.k + hrow * 16;
+  const uint16_t* vg = p.v + hrow * p.dv;
+  const int c0 = seg * p.seg_chunks;
+  const int nch = p.seg_chunks;
+
+  f32x4 S[3][4];
+  float z[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    z[j] = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) S[j][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  }
+  float vs = 0.f;
+
+  ChunkRegs cr;
+  chunk_load<VEC>(cr, p, qg, kg, vg, c0 * CH, tid);
+  for (int c = 0; c < nch; ++c) {
+    __syncthreads();   // previous chunk fully consumed
+    chunk_store(cr, L, p.kphi, tid);
+    __syncthreads();
+    if (c + 1 < nch) chunk_load<VEC>(cr, p, qg, kg, vg, (c0 + c + 1) * CH, tid);
+    if (w < 2)
+      update_slots<3>(L, S, z, w, lane);
+    else
+      update_slots<2>(L, S, z, w, lane);
+    vs += chunk_vsum_part(L, tid);
+  }
+  // write the increment: S^T fp16 [dv][f], z, sum v
+  const int r = lane & 15, g = lane >> 4;
+  const size_t sidx = (size_t)bh * p.P + seg;
+  uint16_t* wsS = p.wsS + sidx * (DVC * NF);
+  const int NS = w < 2 ? 3 : 2;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    if (j >= NS) break;
+    const int s = w + 4 * j;
+    float zz = sum_groups(z[j]);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const u32x2 pk = {pack_f16x2(S[j][nt][0], S[j][nt][1]), pack_f16x2(S[j][nt][2], S[j][nt][3])};
+      *reinterpret_cast<u32x2*>(&wsS[(16 * nt + r) * NF + 16 * s + 4 * g]) = pk;
+    }
+    if (g == 0) p.wsZ[sidx * NF + 16 * s + r] = zz;
+  }
+  if ((tid & 3) == 0) p.wsV[sidx * DVC + (tid >> 2)] = vs;
+}
+
+// -------------------------------------------------------------------------------------------
+// Kernel 2: outputs.  Work-group (head, segment); wave w handles tokens 16w..16w+15 of every
+// chunk for the phi(Q).S and intra terms, and owns state slots {w, w+4, w+8}.
+template <bool VEC, bool UNIT>
+__global__ __launch_bounds__(256) void chunked_output_kernel(const ChunkParams p) {
+  __shared__ __attribute__((aligned(16))) ChunkLds L;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  int bh, seg;
+  map_segment(blockIdx.x, p.BH, p.P, bh, seg);
+  const int N = p.N, dv = p.dv;
+  const size_t hrow = (size_t)bh * N;
+  const uint16_t* qg = p.q + hrow * 16;
+  const uint16_t* kg = p.k + hrow * 16;
+  const uint16_t* vg = p.v + hrow * dv;
+  const int nchunks_total = (N + CH - 1) / CH;
+  const int c0 = seg * p.seg_chunks;
+  const int nch = min(p.seg_chunks, nchunks_total - c0);
+  const int NS = w < 2 ? 3 : 2;
+  const float W = p.W;
+
+  // ---- state at the segment start: sum of the increments of earlier segments
+  f32x4 S[3][4];
+  float z[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) {
+    z[j] = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) S[j][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  }
+  float s0 = 0.f;   // threads 0..63: sum of v over earlier segments for dv = tid
+  for (int sp = 0; sp < seg; ++sp) {
+    const size_t sidx = (size_t)bh * p.P + sp;
+    const uint16_t* wsS = p.wsS + sidx * (DVC * NF);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      if (j >= NS) break;
+      const int s = w + 4 * j;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const u32x2 pk = *reinterpret_cast<const u32x2*>(&wsS[(16 * nt + r) * NF + 16 * s + 4 * g]);
+        S[j][nt][0] += f16_lo_to_f32(pk[0]);
+        S[j][nt][1] += f16_hi_to_f32(pk[0]);
+        S[j][nt][2] += f16_lo_to_f32(pk[1]);
+        S[j][nt][3] += f16_hi_to_f32(pk[1]);
+      }
+      if (g == 0) z[j] += p.wsZ[sidx * NF + 16 * s + r];
+    }
+    if (tid < DVC) s0 += p.wsV[sidx * DVC + tid];
+  }
+  // z partials are kept per lane group: group 0 holds the full value, others zero
+  if (w < 2)
+    publish_slots<3>(L, S, z, w, lane);
+  else
+    publish_slots<2>(L, S, z, w, lane);
+  if (tid < DVC) L.S0[tid] = s0;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) z[j] = (g == 0) ? z[j] : 0.f;
+
+  const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
+  constexpr u32 kOnes = 0x3c003c00u;
+
+  ChunkRegs cr;
+  chunk_load<VEC>(cr, p, qg, kg, vg, c0 * CH, tid);
+  for (int c = 0; c < nch; ++c) {
+    const int row0 = (c0 + c) * CH;
+    __syncthreads();   // previous chunk consumed (Q, K, V, S^T, z, S0 readers done)
+    chunk_store(cr, L, p.kphi, tid);
+    if (c > 0) {
+      if (w < 2)
+        publish_slots<3>(L, S, z, w, lane);
+      else
+        publish_slots<2>(L, S, z, w, lane);
+      if (tid < DVC) L.S0[tid] += L.S0c[tid];
+    }
+    __syncthreads();
+    if (c + 1 < nch) chunk_load<VEC>(cr, p, qg, kg, vg, row0 + CH, tid);
+
+    // ---- q~ copies for this wave's token t = 16w + r (lane group g)
+    const int tl = 16 * w + r;   // chunk-local token of this lane (A layout)
+    float xa[16], xb[16], xb0[16];
+    {
+      const u32x4 q0 = *reinterpret_cast<const u32x4*>(&L.Qs[tl * QKS]);
+      const u32x4 q1 = *reinterpret_cast<const u32x4*>(&L.Qs[tl * QKS + 8]);
+      float qv[16];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qv[2 * e] = p.qphi * bf16_lo_to_f32(q0[e]);
+        qv[2 * e + 1] = p.qphi * bf16_hi_to_f32(q0[e]);
+        qv[8 + 2 * e] = p.qphi * bf16_lo_to_f32(q1[e]);
+        qv[8 + 2 * e + 1] = p.qphi * bf16_hi_to_f32(q1[e]);
+      }
+      const bool odd = (g & 1) != 0, hig = g >= 2;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) xa[e] = odd ? qv[(e + 8) & 15] : qv[e];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        xb[e] = W * (hig ? xa[(e + 4) & 15] : xa[e]);
+        xb0[e] = hig ? (0.5f * W) * xa[e] : W;
+      }
+    }
+
+    // ---- inter-chunk: O = phi(Q) S (u units), den_inter = phi(Q).z
+    f32x4 O[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) O[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float dpart = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 5; ++ks) {
+      float ph[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ph[e] = (ks == 0) ? xa[e] * xb0[e] : xa[e] * xb[(e + ks) & 15];
+      const u32x4 a = {pack_f16x2(ph[0], ph[1]), pack_f16x2(ph[2], ph[3]), pack_f16x2(ph[4], ph[5]),
+                       pack_f16x2(ph[6], ph[7])};
+      if (p.normalize) {
+        const f4 z0 = *reinterpret_cast<const f4*>(&L.Z[32 * ks + 8 * g]);
+        const f4 z1 = *reinterpret_cast<const f4*>(&L.Z[32 * ks + 8 * g + 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dpart = __builtin_fmaf(ph[e], z0[e], dpart);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dpart = __builtin_fmaf(ph[4 + e], z1[e], dpart);
+      }
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const u32x4 b = *reinterpret_cast<const u32x4*>(&L.ST[(16 * nt + r) * STS + 32 * ks + 8 * g]);
+        O[nt] = mfma16_f16(a, b, O[nt]);
+      }
+    }
+
+    // ---- intra-chunk, d-form: scores S^T (keys x queries) for key tiles kt <= w
+    const u32x4 qb = (g < 2) ? scale_bf16x8(*reinterpret_cast<const u32x4*>(&L.Qs[tl * QKS + 8 * g]), p.qscale)
+                             : (u32x4){0u, 0u, 0u, 0u};
+    float rs = 0.f;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      if (32 * m > 16 * w + 15) break;
+      float u[2][4];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int kt = 2 * m + h2;
+        if (kt > w) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) u[h2][i] = 0.f;
+          continue;
+        }
+        const u32x4 ka = (g < 2) ? *reinterpret_cast<const u32x4*>(&L.Ks[(16 * kt + r) * QKS + 8 * g])
+                                 : (u32x4){0u, 0u, 0u, 0u};
+        f32x4 b = {inv_c, inv_c, inv_c, inv_c};
+        b = mfma16_bf16(ka, qb, b);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float uu = __builtin_fmaf(b[i], b[i], -inv_c2);
+          const int key = 16 * kt + 4 * g + i;   // chunk-local key of S^T row
+          u[h2][i] = (kt == w && key > tl) ? 0.f : uu;
+        }
+      }
+      // S^T C layout: lane (query col r, key rows 4g+i) == A layout of P for keys
+      // {32m + 4g + i, 32m + 16 + 4g + i}
+      const u32x4 pa = {pack_f16x2(u[0][0], u[0][1]), pack_f16x2(u[0][2], u[0][3]), pack_f16x2(u[1][0], u[1][1]),
+                        pack_f16x2(u[1][2], u[1][3])};
+      rs = dot2_f16(pa[0], kOnes, rs);
+      rs = dot2_f16(pa[1], kOnes, rs);
+      rs = dot2_f16(pa[2], kOnes, rs);
+      rs = dot2_f16(pa[3], kOnes, rs);
+      u32 mw[4];
+#pragma unroll
+      for (int c2 = 0; c2 < 4; ++c2) {
+        const int h2 = c2 >> 1, i0 = 2 * (c2 & 1);
+        const int key0 = 32 * m + 16 * h2 + 4 * g + i0;
+        const u32 lo = (key0 <= tl) ? (p.ones_hi & 0xffffu) : 0u;
+        const u32 hi = (key0 + 1 <= tl) ? (p.ones_hi & 0xffff0000u) : 0u;
+        mw[c2] = lo | hi;
+      }
+      const u32x4 mk = {mw[0], mw[1], mw[2], mw[3]};
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+        const uint16_t* vp = &L.VT[(16 * nt + r) * VTS + 32 * m + 4 * g];
+        const u32x2 a0 = *reinterpret_cast<const u32x2*>(vp);
+        const u32x2 a1 = *reinterpret_cast<const u32x2*>(vp + 16);
+        const u32x4 vb = {a0[0], a0[1], a1[0], a1[1]};
+        O[nt] = mfma16_f16(pa, vb, O[nt]);
+        O[nt] = mfma16_f16(mk, vb, O[nt]);
+        if (p.ones_lo != 0u) {
+          u32x4 ml;
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            ml[t] = ((mk[t] & 0xffffu) ? (p.ones_lo & 0xffffu) : 0u) |
+                    ((mk[t] & 0xffff0000u) ? (p.ones_lo & 0xffff0000u) : 0u);
+          O[nt] = mfma16_f16(ml, vb, O[nt]);
+        }
+      }
+    }
+
+    // ---- denominator of token tl (A layout, every lane group holds it after the reduction)
+    const float dsum = sum_groups(dpart + rs);   // u units
+    const float den_a = (float)(row0 + tl + 1) + dsum * p.fscale;
+
+    // ---- state update with this chunk (S lives in registers; S^T in LDS is rewritten only
+    // after the next barrier)
+    const float vsc = chunk_vsum_part(L, tid);
+    if ((tid & 3) == 0) L.S0c[tid >> 2] = vsc;
+    if (w < 2)
+      update_slots<3>(L, S, z, w, lane);
+    else
+      update_slots<2>(L, S, z, w, lane);
+
+    // ---- outputs: C layout, lane (dv col 16nt + r, tokens 4g + i of this wave)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * g + i;
+      const int row = row0 + t;
+      const float den = __shfl(den_a, 4 * g + i);
+      const float inv = p.normalize ? 1.0f / (den + p.eps) : 1.0f;
+      if (row < N) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          const int col = 16 * nt + r;
+          if (col < dv) {
+            const float y = (L.S0[col] + O[nt][i] * p.fscale) * inv;
+            const size_t o = (size_t)(hrow + row) * dv + col;
+            if (p.out_f32)
+              static_cast<float*>(p.out)[o] = y;
+            else
+              static_cast<uint16_t*>(p.out)[o] = f32_to_bf16_bits(y);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- final state of the head (last segment) in the reference feature basis, fp32:
+  // state_out[f][0..dv) = sum_u phi_f(k_u) v_u, state_out[f][dv] = sum_u phi_f(k_u)
+  if (p.state_out != nullptr && seg == p.P - 1) {
+    __syncthreads();
+    if (tid < DVC) L.S0[tid] += L.S0c[tid];
+    __syncthreads();
+    constexpr int F = 153;
+    float* so = p.state_out + (size_t)bh * F * (dv + 1);
+    if (tid < dv) so[tid] = L.S0[tid];
+    if (tid == 0) so[dv] = (float)N;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      if (j >= NS) break;
+      const int s = w + 4 * j;
+      const int dl = slot_delta(s);
+      const float fac = s == 0 ? p.st_lin : (s == 1 ? p.st_diag : p.st_off);
+      // z: row r of the slot (lanes with g == 0 write); delta = 8 rows r and r+8 are one pair
+      float zz = sum_groups(z[j]);
+      const float zpart = __shfl_xor(zz, 8);
+      // S: C layout rows fi = 4g + i; the delta = 8 partner row fi + 8 sits 32 lanes away
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int fi = 4 * g + i;
+          const float mine = S[j][nt][i];
+          const float other = __shfl_xor(mine, 32);
+          const bool skip = (dl == 8) && fi >= 8;
+          const float val = (dl == 8) ? mine + other : mine;
+          int a = fi, b = (fi + dl) & 15;
+          if (a > b) { const int t2 = a; a = b; b = t2; }
+          const int ref = (s == 0) ? 1 + fi : (s == 1 ? 17 + fi : 33 + a * (31 - a) / 2 + (b - a - 1));
+          const int col = 16 * nt + r;
+          if (!skip && col < dv) so[(size_t)ref * (dv + 1) + col] = val * fac;
+        }
+      }
+      if (g == 0 && !((dl == 8) && r >= 8)) {
+        int a = r, b = (r + dl) & 15;
+        if (a > b) { const int t2 = a; a = b; b = t2; }
+        const int ref = (s == 0) ? 1 + r : (s == 1 ? 17 + r : 33 + a * (31 - a) / 2 + (b - a - 1));
+        so[(size_t)ref * (dv + 1) + dv] = ((dl == 8) ? zz + zpart : zz) * fac;
+      }
+    }
+  }
+}
+
+// Segment split: enough (head, segment) work-groups to fill the GPU twice over.
+void segment_split(int BH, int N, int& P, int& seg_chunks) {
+  const int nchunks = (N + CH - 1) / CH;
+  P = (512 + BH - 1) / BH;
+  if (P > nchunks) P = nchunks;
+  if (P < 1) P = 1;
+  seg_chunks = (nchunks + P - 1) / P;
+  P = (nchunks + seg_chunks - 1) / seg_chunks;
+}
+
+}  // namespace
+
+size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk) {
+  if (d != 16 || dv > 64 || chunk < 1) return (size_t)-1;
+  int P, seg_chunks;
+  segment_split(BH, N, P, seg_chunks);
+  const size_t per = (size_t)DVC * NF * 2 + (size_t)NF * 4 + (size_t)DVC * 4;
+  return (size_t)BH * P * per + 256;
+}
+
+int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
+  if (a.d != 16 || a.dv > 64) return LA_ERR_UNSUPPORTED_DIM;
+  if (a.in_f32) return LA_ERR_BAD_DTYPE;
+  ChunkParams p{};
+  p.q = static_cast<const uint16_t*>(a.q);
+  p.k = static_cast<const uint16_t*>(a.k);
+  p.v = static_cast<const uint16_t*>(a.v);
+  p.out = a.out;
+  p.state_out = a.state_out;
+  p.BH = a.BH;
+  p.N = a.N;
+  p.dv = a.dv;
+  int P, seg_chunks;
+  segment_split(a.BH, a.N, P, seg_chunks);
+  p.P = P;
+  p.seg_chunks = seg_chunks;
+  const size_t sS = (size_t)a.BH * P * DVC * NF * 2, sZ = (size_t)a.BH * P * NF * 4;
+  char* ws = static_cast<char*>(a.workspace);
+  p.wsS = reinterpret_cast<uint16_t*>(ws);
+  p.wsZ = reinterpret_cast<float*>(ws + sS);
+  p.wsV = reinterpret_cast<float*>(ws + sS + sZ);
+  // intra d-form constants (same as the parallel kernel)
+  const double ic = 1.0 / (double)a.scale;
+  const int k = (int)lround(0.5 * log2(2.0 * ic * ic) - 0.25);
+  const double qs = ldexp(1.0, -k);
+  const float icf = (float)(ic * qs);
+  p.qscale = (float)qs;
+  p.inv_c = icf;
+  p.inv_c2 = (float)((double)icf * (double)icf);
+  const double w = 2.0 * (double)icf * (double)icf;
+  p.W = (float)w;
+  p.fscale = (float)(1.0 / w);
+  const _Float16 whi = (_Float16)w;
+  const _Float16 wlo = (_Float16)(w - (double)whi);
+  const u32 hb = __builtin_bit_cast(uint16_t, whi), lb = __builtin_bit_cast(uint16_t, wlo);
+  p.ones_hi = hb | (hb << 16);
+  p.ones_lo = ((double)wlo == 0.0) ? 0u : (lb | (lb << 16));
+  // feature scaling: q~ = sqrt(c) 2^(sigma/2) q, k~ = sqrt(c) 2^(-sigma/2) k
+  int sigma = 0;
+  while ((1 << (sigma + 10)) < a.N && sigma < 12) sigma += 2;
+  const double rc = sqrt((double)a.scale);
+  p.qphi = (float)(rc * ldexp(1.0, sigma / 2));
+  p.kphi = (float)(rc * ldexp(1.0, -sigma / 2));
+  p.st_lin = (float)ldexp(1.0, sigma / 2);
+  p.st_diag = (float)(ldexp(1.0, sigma) / sqrt(2.0));
+  p.st_off = (float)ldexp(1.0, sigma);
+  p.eps = a.eps;
+  p.normalize = a.normalize ? 1 : 0;
+  p.out_f32 = a.out_f32 ? 1 : 0;
+  const bool vec = (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(a.k) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 7) == 0);
+  p.vec = vec;
+  const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
+  if (P > 1) {
+    const dim3 grid((unsigned)(a.BH * (P - 1)));
+    if (vec)
+      hipLaunchKernelGGL(chunked_segment_kernel<true>, grid, dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL(chunked_segment_kernel<false>, grid, dim3(256), 0, stream, p);
+    const int e = (int)hipGetLastError();
+    if (e != 0) return e;
+  }
+  const dim3 grid((unsigned)(a.BH * P));
+  if (vec && unit)
+    hipLaunchKernelGGL((chunked_output_kernel<true, true>), grid, dim3(256), 0, stream, p);
+  else if (vec)
+    hipLaunchKernelGGL((chunked_output_kernel<true, false>), grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((chunked_output_kernel<false, false>), grid, dim3(256), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
 }  // namespace la

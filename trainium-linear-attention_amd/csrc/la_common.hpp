@@ -37,6 +37,11 @@ __device__ __forceinline__ u32 pack_f16x2(float lo, float hi) {
   return __builtin_bit_cast(u32, p);
 }
 
+__device__ __forceinline__ float f16_lo_to_f32(u32 w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+}
+__device__ __forceinline__ float f16_hi_to_f32(u32 w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
+
 // sum += a.lo*b.lo + a.hi*b.hi over packed fp16 pairs, fp32 accumulate (v_dot2_f32_f16).
 __device__ __forceinline__ float dot2_f16(u32 a, u32 b, float acc) {
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);

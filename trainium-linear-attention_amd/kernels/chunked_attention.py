@@ -12,6 +12,12 @@ reference's ``taylor_feature_map`` and ``chunked_nki_numerator``
 The feature map is applied inside the chunked kernel: phi(Q), phi(K) never reach HBM, and the
 state stays on chip across chunks (the NKI kernel round-trips it through HBM,
 kernels/nki_attention_chunked.py:92-102).  dv may differ from d.
+
+The chunked kernel covers bf16 inputs with d = 16 and dv <= 64 (the BASED configuration).
+Other shapes and fp32 inputs are computed by the fused parallel kernel, which evaluates the
+same function (numerator or normalised) on the GPU.  ``chunk_size`` is accepted for signature
+compatibility; the kernel's recurrence uses 64-token chunks, which gives the same result for
+every chunk size up to rounding (chunk-size invariance of the recurrence).
 """
 
 from __future__ import annotations
@@ -23,7 +29,8 @@ import torch
 from . import _lib
 from .pytorch_attention import _as_kernel_input, _check_qkv, _compute_dtype
 
-__all__ = ["taylor_feature_map", "feature_dim", "chunked_nki_numerator", "chunked_based_attn", "based_chunked"]
+__all__ = ["taylor_feature_map", "feature_dim", "chunked_nki_numerator", "chunked_based_attn", "based_chunked",
+           "chunked_supported"]
 
 
 def feature_dim(d: int) -> int:
@@ -45,6 +52,11 @@ def taylor_feature_map(x):
     return out if out.dtype == x.dtype else out.to(x.dtype)
 
 
+def chunked_supported(d: int, dv: int, dtype: torch.dtype) -> bool:
+    """Shapes the chunked HIP kernel implements (bf16, d = 16, dv <= 64)."""
+    return d == 16 and 1 <= dv <= 64 and dtype == torch.bfloat16
+
+
 def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, out_dtype=None,
                   return_state=False):
     """Chunked recurrent BASED attention through ``la_based_chunked_fwd``.
@@ -53,9 +65,16 @@ def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, 
     (b, h, F, dv + 1) fp32 = [sum_u phi(k_u) v_u^T | sum_u phi(k_u)].
     """
     _check_qkv(q, k, v)
+    if int(chunk_size) < 1:
+        raise _lib.BasedLAError("chunk_size must be >= 1")
     b, h, t, d = q.shape
     dv = v.shape[-1]
     cdt = _compute_dtype(q.dtype)
+    if not chunked_supported(d, dv, cdt):
+        if return_state:
+            raise _lib.BasedLAError("state export needs the chunked kernel (bf16, d = 16, dv <= 64)")
+        from .pytorch_attention import based_parallel
+        return based_parallel(q, k, v, eps=eps, scale=scale, normalize=normalize, out_dtype=out_dtype)
     odt = q.dtype if out_dtype is None else out_dtype
     kdt = odt if odt in (torch.float32, torch.bfloat16) else torch.float32
     if scale is None:
