@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--configs", choices=["all", "none"], default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-heads", type=int, default=2)
+    ap.add_argument("--only", default=None,
+                    help="comma-separated configuration names (or 'headline') to measure alone, e.g. for profiling")
     return ap.parse_args()
 
 
@@ -249,6 +251,14 @@ def main():
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
 
+    if args.only:
+        names = set(args.only.split(","))
+        res = {}
+        for cfg in [HEADLINE] + CONFIGS:
+            if cfg[0] in names or (cfg is HEADLINE and "headline" in names):
+                res[cfg[0]] = measure(cfg, args.steps, args.warmup, args.rotate, device)
+        print(json.dumps({"only": res}))
+        return
     head = measure(HEADLINE, args.steps, args.warmup, args.rotate, device)
     per_config = {}
     if args.configs == "all":

@@ -106,15 +106,16 @@ struct ChunkRegs {
   u32x2 v[4];        // 4 tokens x 4 dv of V
 };
 
-template <bool VEC>
+// QK: load q (threads 0..127) and k (128..255); otherwise only k (threads 0..127).
+template <bool VEC, bool QK>
 __device__ __forceinline__ void chunk_load(ChunkRegs& r, const ChunkParams& p, const uint16_t* qg, const uint16_t* kg,
                                            const uint16_t* vg, int row0, int tid) {
   const int N = p.N, dv = p.dv;
   {
     const int t = tid & 127, row = row0 + (t >> 1), col = 8 * (t & 1);
-    const uint16_t* base = (tid < 128) ? qg : kg;
+    const uint16_t* base = QK ? ((tid < 128) ? qg : kg) : kg;
     u32x4 x = {0u, 0u, 0u, 0u};
-    if (row < N) {
+    if (row < N && (QK || tid < 128)) {
       const uint16_t* src = base + (size_t)row * 16 + col;
       if (VEC) {
         x = *reinterpret_cast<const u32x4*>(src);
@@ -150,13 +151,14 @@ __device__ __forceinline__ void chunk_load(ChunkRegs& r, const ChunkParams& p, c
   }
 }
 
+template <bool QK>
 __device__ __forceinline__ void chunk_store(const ChunkRegs& r, ChunkLds& L, float kphi, int tid) {
   {
     const int t = tid & 127, row = t >> 1, col = 8 * (t & 1);
-    if (tid < 128) {
+    if (QK && tid < 128) {
       *reinterpret_cast<u32x4*>(&L.Qs[row * QKS + col]) = r.qk;
-    } else {
-      *reinterpret_cast<u32x4*>(&L.Ks[row * QKS + col]) = r.qk;
+    } else if (QK || tid < 128) {
+      if (QK) *reinterpret_cast<u32x4*>(&L.Ks[row * QKS + col]) = r.qk;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         L.KT[(col + 2 * e) * KTS + row] = kphi * bf16_lo_to_f32(r.qk[e]);
@@ -278,9 +280,9 @@ __device__ __forceinline__ void publish_slots(ChunkLds& L, const f32x4 (&S)[3][4
 // -------------------------------------------------------------------------------------------
 // Kernel 1: per (head, segment < P-1) state increment of the segment.
 template <bool VEC>
-__global__ __launch_bounds__(256) void chunked_segment_kernel(const ChunkParams p) {
+__global__ __launch_bounds__(256, 2) void chunked_segment_kernel(const ChunkParams p) {
   __shared__ __attribute__((aligned(16))) ChunkLds L;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   int bh, seg;
   map_segment(blockIdx.x, p.BH, p.P - 1, bh, seg);
   const size_t hrow = (size_t)bh * p.N;
@@ -300,18 +302,24 @@ __global__ __launch_bounds__(256) void chunked_segment_kernel(const ChunkParams 
   }
   float vs = 0.f;
 
-  ChunkRegs cr;
-  chunk_load<VEC>(cr, p, qg, kg, vg, c0 * CH, tid);
-  for (int c = 0; c < nch; ++c) {
+  // two chunks in flight: chunk c is stored from its registers, then chunk c + 2 is loaded into them
+  ChunkRegs ra, rb;
+  chunk_load<VEC, false>(ra, p, qg, kg, vg, c0 * CH, tid);
+  if (nch > 1) chunk_load<VEC, false>(rb, p, qg, kg, vg, (c0 + 1) * CH, tid);
+  auto step = [&](ChunkRegs& cur, int c) {
     __syncthreads();   // previous chunk fully consumed
-    chunk_store(cr, L, p.kphi, tid);
+    chunk_store<false>(cur, L, p.kphi, tid);
     __syncthreads();
-    if (c + 1 < nch) chunk_load<VEC>(cr, p, qg, kg, vg, (c0 + c + 1) * CH, tid);
+    if (c + 2 < nch) chunk_load<VEC, false>(cur, p, qg, kg, vg, (c0 + c + 2) * CH, tid);
     if (w < 2)
       update_slots<3>(L, S, z, w, lane);
     else
       update_slots<2>(L, S, z, w, lane);
     vs += chunk_vsum_part(L, tid);
+  };
+  for (int c = 0; c < nch; c += 2) {
+    step(ra, c);
+    if (c + 1 < nch) step(rb, c + 1);
   }
   // write the increment: S^T fp16 [dv][f], z, sum v
   const int r = lane & 15, g = lane >> 4;
@@ -334,12 +342,44 @@ __global__ __launch_bounds__(256) void chunked_segment_kernel(const ChunkParams 
 }
 
 // -------------------------------------------------------------------------------------------
+// Kernel 1b: exclusive prefix over segments, in place.  Thread (head, element); after it, slot
+// p - 1 holds sum_{p' < p} of the increments (S as fp16, z and sum v as fp32).
+__global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p) {
+  constexpr int NS_ELEM = DVC * NF, NE = NS_ELEM + NF + DVC;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  const int bh = blockIdx.y;
+  if (e >= NE) return;
+  const int nseg = p.P - 1;
+  float acc = 0.f;
+  if (e < NS_ELEM) {
+    uint16_t* base = p.wsS + (size_t)bh * p.P * NS_ELEM + e;
+    for (int sp = 0; sp < nseg; ++sp) {
+      uint16_t* ptr = base + (size_t)sp * NS_ELEM;
+      acc += (float)__builtin_bit_cast(_Float16, *ptr);
+      *ptr = __builtin_bit_cast(uint16_t, (_Float16)acc);
+    }
+  } else if (e < NS_ELEM + NF) {
+    float* base = p.wsZ + (size_t)bh * p.P * NF + (e - NS_ELEM);
+    for (int sp = 0; sp < nseg; ++sp) {
+      acc += base[(size_t)sp * NF];
+      base[(size_t)sp * NF] = acc;
+    }
+  } else {
+    float* base = p.wsV + (size_t)bh * p.P * DVC + (e - NS_ELEM - NF);
+    for (int sp = 0; sp < nseg; ++sp) {
+      acc += base[(size_t)sp * DVC];
+      base[(size_t)sp * DVC] = acc;
+    }
+  }
+}
+
+// -------------------------------------------------------------------------------------------
 // Kernel 2: outputs.  Work-group (head, segment); wave w handles tokens 16w..16w+15 of every
 // chunk for the phi(Q).S and intra terms, and owns state slots {w, w+4, w+8}.
 template <bool VEC, bool UNIT>
-__global__ __launch_bounds__(256) void chunked_output_kernel(const ChunkParams p) {
+__global__ __launch_bounds__(256, 2) void chunked_output_kernel(const ChunkParams p) {
   __shared__ __attribute__((aligned(16))) ChunkLds L;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
   int bh, seg;
   map_segment(blockIdx.x, p.BH, p.P, bh, seg);
@@ -364,8 +404,9 @@ __global__ __launch_bounds__(256) void chunked_output_kernel(const ChunkParams p
     for (int nt = 0; nt < 4; ++nt) S[j][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
   }
   float s0 = 0.f;   // threads 0..63: sum of v over earlier segments for dv = tid
-  for (int sp = 0; sp < seg; ++sp) {
-    const size_t sidx = (size_t)bh * p.P + sp;
+  if (seg > 0) {
+    // the prefix kernel left sum_{p' < seg} of the increments in slot seg - 1
+    const size_t sidx = (size_t)bh * p.P + (seg - 1);
     const uint16_t* wsS = p.wsS + sidx * (DVC * NF);
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
@@ -374,14 +415,14 @@ __global__ __launch_bounds__(256) void chunked_output_kernel(const ChunkParams p
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const u32x2 pk = *reinterpret_cast<const u32x2*>(&wsS[(16 * nt + r) * NF + 16 * s + 4 * g]);
-        S[j][nt][0] += f16_lo_to_f32(pk[0]);
-        S[j][nt][1] += f16_hi_to_f32(pk[0]);
-        S[j][nt][2] += f16_lo_to_f32(pk[1]);
-        S[j][nt][3] += f16_hi_to_f32(pk[1]);
+        S[j][nt][0] = f16_lo_to_f32(pk[0]);
+        S[j][nt][1] = f16_hi_to_f32(pk[0]);
+        S[j][nt][2] = f16_lo_to_f32(pk[1]);
+        S[j][nt][3] = f16_hi_to_f32(pk[1]);
       }
-      if (g == 0) z[j] += p.wsZ[sidx * NF + 16 * s + r];
+      if (g == 0) z[j] = p.wsZ[sidx * NF + 16 * s + r];
     }
-    if (tid < DVC) s0 += p.wsV[sidx * DVC + tid];
+    if (tid < DVC) s0 = p.wsV[sidx * DVC + tid];
   }
   // z partials are kept per lane group: group 0 holds the full value, others zero
   if (w < 2)
@@ -395,12 +436,12 @@ __global__ __launch_bounds__(256) void chunked_output_kernel(const ChunkParams p
   const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
   constexpr u32 kOnes = 0x3c003c00u;
 
-  ChunkRegs cr;
-  chunk_load<VEC>(cr, p, qg, kg, vg, c0 * CH, tid);
+  ChunkRegs cur;
+  chunk_load<VEC, true>(cur, p, qg, kg, vg, c0 * CH, tid);
   for (int c = 0; c < nch; ++c) {
     const int row0 = (c0 + c) * CH;
     __syncthreads();   // previous chunk consumed (Q, K, V, S^T, z, S0 readers done)
-    chunk_store(cr, L, p.kphi, tid);
+    chunk_store<true>(cur, L, p.kphi, tid);
     if (c > 0) {
       if (w < 2)
         publish_slots<3>(L, S, z, w, lane);
@@ -409,30 +450,41 @@ __global__ __launch_bounds__(256) void chunked_output_kernel(const ChunkParams p
       if (tid < DVC) L.S0[tid] += L.S0c[tid];
     }
     __syncthreads();
-    if (c + 1 < nch) chunk_load<VEC>(cr, p, qg, kg, vg, row0 + CH, tid);
+    if (c + 1 < nch) chunk_load<VEC, true>(cur, p, qg, kg, vg, row0 + CH, tid);
 
-    // ---- q~ copies for this wave's token t = 16w + r (lane group g)
+    // ---- q~ copies for this wave's token t = 16w + r (lane group g), rotated through the
+    // LDS address (no register-indexed selects):
+    //   xa[e] = q~[(e + 8*odd) % 16],  xb[e] = W * q~[(e + 8*odd + 4*hig) % 16],
+    //   xb0[e] = hig ? (W/2) xa[e] : W
     const int tl = 16 * w + r;   // chunk-local token of this lane (A layout)
     float xa[16], xb[16], xb0[16];
     {
-      const u32x4 q0 = *reinterpret_cast<const u32x4*>(&L.Qs[tl * QKS]);
-      const u32x4 q1 = *reinterpret_cast<const u32x4*>(&L.Qs[tl * QKS + 8]);
-      float qv[16];
+      const int odd = g & 1, hig = g >> 1;
+      const uint16_t* qrow = &L.Qs[tl * QKS];
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(qrow + 8 * odd);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(qrow + 8 * (1 - odd));
+      const int rb = 8 * odd + 4 * hig;
+      u32x2 b[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) b[t] = *reinterpret_cast<const u32x2*>(qrow + ((rb + 4 * t) & 15));
+      const float qp = p.qphi, qw = p.qphi * W;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        qv[2 * e] = p.qphi * bf16_lo_to_f32(q0[e]);
-        qv[2 * e + 1] = p.qphi * bf16_hi_to_f32(q0[e]);
-        qv[8 + 2 * e] = p.qphi * bf16_lo_to_f32(q1[e]);
-        qv[8 + 2 * e + 1] = p.qphi * bf16_hi_to_f32(q1[e]);
+        xa[2 * e] = qp * bf16_lo_to_f32(a0[e]);
+        xa[2 * e + 1] = qp * bf16_hi_to_f32(a0[e]);
+        xa[8 + 2 * e] = qp * bf16_lo_to_f32(a1[e]);
+        xa[8 + 2 * e + 1] = qp * bf16_hi_to_f32(a1[e]);
       }
-      const bool odd = (g & 1) != 0, hig = g >= 2;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) xa[e] = odd ? qv[(e + 8) & 15] : qv[e];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        xb[e] = W * (hig ? xa[(e + 4) & 15] : xa[e]);
-        xb0[e] = hig ? (0.5f * W) * xa[e] : W;
+      for (int t = 0; t < 4; ++t) {
+        xb[4 * t] = qw * bf16_lo_to_f32(b[t][0]);
+        xb[4 * t + 1] = qw * bf16_hi_to_f32(b[t][0]);
+        xb[4 * t + 2] = qw * bf16_lo_to_f32(b[t][1]);
+        xb[4 * t + 3] = qw * bf16_hi_to_f32(b[t][1]);
       }
+      const float ca = hig ? 0.5f * W : 0.f, cb = hig ? 0.f : W;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xb0[e] = __builtin_fmaf(xa[e], ca, cb);
     }
 
     // ---- inter-chunk: O = phi(Q) S (u units), den_inter = phi(Q).z
@@ -688,7 +740,11 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
       hipLaunchKernelGGL(chunked_segment_kernel<true>, grid, dim3(256), 0, stream, p);
     else
       hipLaunchKernelGGL(chunked_segment_kernel<false>, grid, dim3(256), 0, stream, p);
-    const int e = (int)hipGetLastError();
+    int e = (int)hipGetLastError();
+    if (e != 0) return e;
+    const dim3 pgrid((unsigned)((DVC * NF + NF + DVC + 255) / 256), (unsigned)a.BH);
+    hipLaunchKernelGGL(chunked_prefix_kernel, pgrid, dim3(256), 0, stream, p);
+    e = (int)hipGetLastError();
     if (e != 0) return e;
   }
   const dim3 grid((unsigned)(a.BH * P));

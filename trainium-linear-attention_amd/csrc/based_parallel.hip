@@ -64,7 +64,7 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
   __shared__ __attribute__((aligned(16))) float snap[NSNAP][DV * LPR];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, n = lane & 31;
   const int N = p.N, d = p.d, dv = p.dv;
 
   int bh, qb;

@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void f32_attn_kernel(const F32Params p) {
   __shared__ __attribute__((aligned(16))) float VTs[2][DV * VROWF];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, n = lane & 31;
   const int N = p.N, d = p.d, dv = p.dv, W = p.window;
   int bh, qb;
   map_causal_block(blockIdx.x, p.BH, p.nqb, bh, qb);

@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void sliding_bf16_kernel(const SlidingParams p
   __shared__ __attribute__((aligned(16))) uint16_t VTs[2][DV * VROW];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, n = lane & 31;
   const int N = p.N, d = p.d, dv = p.dv, W = p.window;
 
   int bh, qb;
