@@ -51,20 +51,28 @@ struct ParallelParams {
 
 // UNIT: 1/c scales to exactly 1 (scale = 1/sqrt(d) with d a power of 4), so the score MFMA
 // starts from the inline constant 1.0 and u = b*b - 1.
-template <int KS, int MT, int QT, bool VEC, bool UNIT>
-__global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const ParallelParams p) {
+//
+// DMA (d = 16, dv % 8 == 0): K and V blocks are copied global -> LDS by buffer_load ... lds
+// (no staging registers, out-of-range rows read as zero) three blocks ahead into four raw
+// stages; V is converted to fp16 and transposed LDS -> LDS one block ahead.  Barriers are
+// plain s_barrier with explicit vmcnt / lgkmcnt waits so that in-flight copies are not drained.
+template <int KS, int MT, int QT, bool VEC, bool UNIT, bool DMA, class KsT, class VTsT, class SnapT, class KrawT,
+          class VrawT>
+__device__ __forceinline__ void based_parallel_body(const ParallelParams& p, KsT* __restrict__ Ks,
+                                                    VTsT* __restrict__ VTs, SnapT* __restrict__ snap,
+                                                    KrawT* __restrict__ Kraw, VrawT* __restrict__ Vraw) {
   constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128 * QT, NSNAP = BM / BN;
   constexpr int KROW = DK + 8;
   constexpr int LPR = 256 / DV;      // threads per V^T row in the running column sum
   constexpr int KPL = BN / LPR;      // keys per thread in the running column sum
   using Stager = BlockStager<KS, MT, VEC, true>;
-
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BN * KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t VTs[2][DV * VROW];
-  __shared__ __attribute__((aligned(16))) float snap[NSNAP][DV * LPR];
+  static_assert(!DMA || KS == 1, "DMA staging is for d = 16");
+  constexpr int NRAW = 4;                 // raw DMA stages
+  constexpr int NKU = 2, NVU = DV / 8;    // 1 KB DMA units per block (K, V)
+  constexpr int NU = NKU + NVU;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, n = lane & 31;
+  const int lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
   const int N = p.N, d = p.d, dv = p.dv;
 
   int bh, qb;
@@ -120,17 +128,112 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
   float vacc = 0.f;
   constexpr u32 kOnes = 0x3c003c00u;  // packed fp16 (1, 1)
 
-  Stager st;
-  st.load(kg, vg, 0, N, d, dv, tid);
-  st.store(Ks[0], VTs[0], tid);
-  if (jb0 == 0) snap[0][tid] = 0.f;
-  __syncthreads();
-
   const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
+
+  // ---- DMA staging helpers
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const int my_units = NU / 4 + (wu < NU % 4 ? 1 : 0);
+  const u32x4 rk = buffer_rsrc(kg, (u32)N * 32u);
+  const u32x4 rv = buffer_rsrc(vg, (u32)N * (u32)dv * 2u);
+  auto issue_dma = [&](int blk) {
+    const int st = blk & (NRAW - 1);
+    const int row0 = blk * BN;
+#pragma unroll
+    for (int i = 0; i < (NU + 3) / 4; ++i) {
+      const int u = wu + 4 * i;
+      if (u >= NU) break;
+      if (u < NKU) {
+        // K slot sl = 2 key + (c ^ ((key >> 2) & 1)): 16-byte chunk c of key row, swizzled
+        const int sl = 64 * u + lane, key = sl >> 1, c = (sl & 1) ^ ((key >> 2) & 1);
+        lds_copy16(rk, lds_addr(&Kraw[st][512 * u]), ((row0 + key) * 16 + 8 * c) * 2);
+      } else {
+        const int ch = 64 * (u - NKU) + lane, key = ch / (DV / 8), col = 8 * (ch % (DV / 8));
+        const int off = col < dv ? ((row0 + key) * dv + col) * 2 : 0x7ffffff0;
+        lds_copy16(rv, lds_addr(&Vraw[st][512 * (u - NKU)]), off);
+      }
+    }
+  };
+  // raw V of block blk (bf16 [key][DV]) -> VTs[blk & 1] (fp16 [dv][key])
+  auto convert_v = [&](int blk) {
+    const uint16_t* src = &Vraw[blk & (NRAW - 1)][0];
+    uint16_t* dstb = &VTs[blk & 1][0];
+#pragma unroll
+    for (int g = tid; g < (DV / 4) * (BN / 4); g += 256) {
+      const int g4 = g % (DV / 4), kg4 = g / (DV / 4);
+      u32x2 x[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = *reinterpret_cast<const u32x2*>(&src[(4 * kg4 + i) * DV + 4 * g4]);
+      const u32 a0 = x[0][0], a1 = x[1][0], a2 = x[2][0], a3 = x[3][0];
+      const u32 b0 = x[0][1], b1 = x[1][1], b2 = x[2][1], b3 = x[3][1];
+      uint16_t* dst = dstb + (4 * g4) * VROW + 4 * kg4;
+      *reinterpret_cast<u32x2*>(dst) = (u32x2){pack_f16x2(bf16_lo_to_f32(a0), bf16_lo_to_f32(a1)),
+                                               pack_f16x2(bf16_lo_to_f32(a2), bf16_lo_to_f32(a3))};
+      *reinterpret_cast<u32x2*>(dst + VROW) = (u32x2){pack_f16x2(bf16_hi_to_f32(a0), bf16_hi_to_f32(a1)),
+                                                      pack_f16x2(bf16_hi_to_f32(a2), bf16_hi_to_f32(a3))};
+      *reinterpret_cast<u32x2*>(dst + 2 * VROW) = (u32x2){pack_f16x2(bf16_lo_to_f32(b0), bf16_lo_to_f32(b1)),
+                                                          pack_f16x2(bf16_lo_to_f32(b2), bf16_lo_to_f32(b3))};
+      *reinterpret_cast<u32x2*>(dst + 3 * VROW) = (u32x2){pack_f16x2(bf16_hi_to_f32(b0), bf16_hi_to_f32(b1)),
+                                                          pack_f16x2(bf16_hi_to_f32(b2), bf16_hi_to_f32(b3))};
+    }
+  };
+  // LDS-only barrier: my LDS writes done, then s_barrier; the asm clobbers keep the compiler
+  // from moving memory operations across it.
+  auto lds_barrier = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0), vmcnt/expcnt unchanged
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // wait until at most `left` DMA units of this wave are still in flight
+  auto wait_dma = [&](int left) {
+    asm volatile("" ::: "memory");
+    if (left >= 6) __builtin_amdgcn_s_waitcnt(0x0f76);
+    else if (left == 5) __builtin_amdgcn_s_waitcnt(0x0f75);
+    else if (left == 4) __builtin_amdgcn_s_waitcnt(0x0f74);
+    else if (left == 3) __builtin_amdgcn_s_waitcnt(0x0f73);
+    else if (left == 2) __builtin_amdgcn_s_waitcnt(0x0f72);
+    else if (left == 1) __builtin_amdgcn_s_waitcnt(0x0f71);
+    else __builtin_amdgcn_s_waitcnt(0x0f70);
+    asm volatile("" ::: "memory");
+  };
+  auto kfrag = [&](int j, int ks, int kk) -> u32x4 {
+    if (DMA) {
+      const int key = 32 * ks + n;
+      const int sl = 2 * key + (h ^ ((key >> 2) & 1));
+      return *reinterpret_cast<const u32x4*>(&Kraw[j & (NRAW - 1)][8 * sl]);
+    }
+    return *reinterpret_cast<const u32x4*>(&Ks[j & 1][(32 * ks + n) * KROW + 16 * kk + 8 * h]);
+  };
+
+  Stager st;
+  if (DMA) {
+    // drain the Q loads so only DMA units are counted by vmcnt from here on
+    __builtin_amdgcn_s_waitcnt(0x0f70);
+    issue_dma(0);
+    if (nblk > 1) issue_dma(1);
+    if (nblk > 2) issue_dma(2);
+    wait_dma(my_units * ((nblk > 2) ? 2 : (nblk > 1 ? 1 : 0)));
+    lds_barrier();
+    convert_v(0);
+    if (jb0 == 0) snap[0][tid] = 0.f;
+  } else {
+    st.load(kg, vg, 0, N, d, dv, tid);
+    st.store(Ks[0], VTs[0], tid);
+    if (jb0 == 0) snap[0][tid] = 0.f;
+    __syncthreads();
+  }
 
   for (int j = 0; j < nblk; ++j) {
     const int s = j & 1;
-    if (j + 1 < nblk) st.load(kg, vg, (j + 1) * BN, N, d, dv, tid);
+    if (DMA) {
+      // block j+1 must have landed; blocks j+2 (and j+3 once issued) may still be in flight
+      wait_dma(j + 2 < nblk ? my_units : 0);
+      lds_barrier();
+      if (j + 3 < nblk) issue_dma(j + 3);
+      if (j + 1 < nblk) convert_v(j + 1);
+    } else {
+      if (j + 1 < nblk) st.load(kg, vg, (j + 1) * BN, N, d, dv, tid);
+    }
 
     if (j <= jb0 + NSNAP - 2) {
       const uint16_t* src = &VTs[s][vs_row * VROW + vs_seg * KPL];
@@ -152,8 +255,7 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
       for (int ks = 0; ks < 2; ++ks) {
         u32x4 kf[KS];
 #pragma unroll
-        for (int kk = 0; kk < KS; ++kk)
-          kf[kk] = *reinterpret_cast<const u32x4*>(&Ks[s][(32 * ks + n) * KROW + 16 * kk + 8 * h]);
+        for (int kk = 0; kk < KS; ++kk) kf[kk] = kfrag(j, ks, kk);
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
           f32x16 b = splat16(inv_c);
@@ -196,8 +298,7 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
         if (kb > wq0 + 32 * QT - 1) break;
         u32x4 kf[KS];
 #pragma unroll
-        for (int kk = 0; kk < KS; ++kk)
-          kf[kk] = *reinterpret_cast<const u32x4*>(&Ks[s][(32 * ks + n) * KROW + 16 * kk + 8 * h]);
+        for (int kk = 0; kk < KS; ++kk) kf[kk] = kfrag(j, ks, kk);
 
         u32x4 pf[QT][2];
         u32x4 mk[QT][2];
@@ -281,9 +382,12 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
       }
     }
 
-    if (j + 1 < nblk) st.store(Ks[s ^ 1], VTs[s ^ 1], tid);
-    __syncthreads();
+    if (!DMA) {
+      if (j + 1 < nblk) st.store(Ks[s ^ 1], VTs[s ^ 1], tid);
+      __syncthreads();
+    }
   }
+  if (DMA) lds_barrier();   // snapshots written in the last iterations
 
   if (!wave_live) return;
 
@@ -344,6 +448,20 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
   }
 }
 
+template <int KS, int MT, int QT, bool VEC, bool UNIT, bool DMA>
+__global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const ParallelParams p) {
+  constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128 * QT, NSNAP = BM / BN;
+  constexpr int KROW = DK + 8;
+  constexpr int LPR = 256 / DV;
+  constexpr int NRAW = 4;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[DMA ? 1 : 2][DMA ? 8 : BN * KROW];
+  __shared__ __attribute__((aligned(16))) uint16_t VTs[2][DV * VROW];
+  __shared__ __attribute__((aligned(16))) float snap[NSNAP][DV * LPR];
+  __shared__ __attribute__((aligned(16))) uint16_t Kraw[DMA ? NRAW : 1][DMA ? BN * 16 : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t Vraw[DMA ? NRAW : 1][DMA ? BN * DV : 8];
+  based_parallel_body<KS, MT, QT, VEC, UNIT, DMA>(p, Ks, VTs, snap, Kraw, Vraw);
+}
+
 template <int KS, int MT, int QT>
 int launch_bf16(const ParallelParams& pp, bool vec, hipStream_t stream) {
   constexpr int BM = 128 * QT;
@@ -351,12 +469,24 @@ int launch_bf16(const ParallelParams& pp, bool vec, hipStream_t stream) {
   p.nqb = (p.N + BM - 1) / BM;
   const dim3 grid((unsigned)(p.nqb * p.BH)), block(256);
   const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
+  // buffer offsets are 32-bit: one head's K and V must stay below 2^31 bytes
+  const bool dma = vec && p.d == 16 && (p.dv % 8) == 0 && (long long)p.N * p.dv * 2 < (1ll << 30);
+  if constexpr (KS == 1 && MT <= 2) {
+    if (dma && unit) {
+      hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, true, true>), grid, block, 0, stream, p);
+      return (int)hipGetLastError();
+    }
+    if (dma) {
+      hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, false, true>), grid, block, 0, stream, p);
+      return (int)hipGetLastError();
+    }
+  }
   if (vec && unit)
-    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, true>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, true, false>), grid, block, 0, stream, p);
   else if (vec)
-    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, false, false>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, false, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, false, false, false>), grid, block, 0, stream, p);
   return (int)hipGetLastError();
 }
 

@@ -99,4 +99,35 @@ __device__ __forceinline__ f32x16 splat16(float x) {
 // Row (key / dv index) of element i of a 32x32 accumulator held by lane group h.
 __device__ __forceinline__ int c32_row(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
 
+// ---- global -> LDS copies (buffer_load_dwordx4 ... lds)
+//
+// A raw buffer descriptor over [base, base + bytes): stride 0, num_records in bytes; dword 3
+// selects raw (untyped) addressing with per-dword range checking, so bytes at or past the end
+// read as zero.  base and bytes must be wave-uniform.
+__device__ __forceinline__ u32x4 buffer_rsrc(const void* base, u32 bytes) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+  return (u32x4){(u32)__builtin_amdgcn_readfirstlane((int)(u32)a),
+                 (u32)__builtin_amdgcn_readfirstlane((int)(u32)(a >> 32)) & 0xffffu,
+                 (u32)__builtin_amdgcn_readfirstlane((int)bytes), 0x00020000u};
+}
+
+// Lane i copies the 16 bytes at byte offset voff of the buffer to LDS address lds_base + 16 i
+// (lds_base wave-uniform).  Issued as inline assembly so that the compiler's wait-count pass does
+// not treat every later LDS read as dependent on the copy: the caller orders copies and reads
+// itself, with s_waitcnt vmcnt and a barrier.  Each call adds one to the wave's vmcnt.
+__device__ __forceinline__ void lds_copy16(const u32x4& rsrc, u32 lds_base, int voff) {
+  asm volatile(
+      "s_nop 0\n\t"   // M0 written by SALU just before an LDS copy needs one wait state
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
+      :
+      : "v"(voff), "s"(rsrc), "{m0}"(lds_base)
+      : "memory");
+}
+
+// LDS byte address of a __shared__ object.
+template <class T>
+__device__ __forceinline__ u32 lds_addr(const T* p) {
+  return (u32)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 }  // namespace la
