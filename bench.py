@@ -120,6 +120,10 @@ class Call:
         self.scale = 1.0 / math.sqrt(d)
         self.ws = None
         self.ws_bytes = 0
+        if kind == "parallel":
+            nb = int(self.L.la_based_parallel_workspace_bytes(B, H, N, d, dv, self.dt))
+            self.ws_bytes = nb
+            self.ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=q.device) if nb else None
         if kind == "chunked":
             nb = int(self.L.la_based_chunked_workspace_bytes(B, H, N, d, dv, chunk))
             if nb == (1 << 64) - 1:
@@ -134,6 +138,7 @@ class Call:
         if self.kind == "parallel":
             rc = L.la_based_parallel_fwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dt,
                                          self.out.data_ptr(), self.odt, None, B, H, N, d, dv, self.scale, 1e-6, 1,
+                                         self.ws.data_ptr() if self.ws is not None else None, self.ws_bytes,
                                          self.stream)
         elif self.kind == "chunked":
             rc = L.la_based_chunked_fwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dt,

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 1
+#define LA_ABI_VERSION 2
 
 /* element types */
 #define LA_F32 0
@@ -56,13 +56,18 @@ const char* la_status_string(int status);
  *
  * q, k: (B,H,N,d); v, out: (B,H,N,dv); in_dtype / out_dtype: LA_BF16 or LA_F32 (q, k and v
  * share in_dtype).  den_or_null: optional (B,H,N) fp32 output of den_t (without eps).
+ * workspace: device scratch of at least la_based_parallel_workspace_bytes(...) bytes, 16-byte
+ * aligned (may be NULL when that is 0).  It holds V repacked as fp16 V^T blocks for the
+ * bf16, d = 16, dv % 8 == 0, dv <= 64 kernel; its contents on return are unspecified.
  * Limits: 1 <= d <= 128, 1 <= dv <= 128, scale > 0 and finite, eps >= 0 and finite.
  * The reference passes scale = 1/sqrt(d) and eps = 1e-6.
  */
+size_t la_based_parallel_workspace_bytes(int B, int H, int N, int d, int dv, int in_dtype);
 int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dtype,
                           void* out, int out_dtype, float* den_or_null,
                           int B, int H, int N, int d, int dv,
-                          float scale, float eps, int normalize, void* hip_stream);
+                          float scale, float eps, int normalize,
+                          void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /*
  * Chunked recurrent BASED attention (linear in N).

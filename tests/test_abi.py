@@ -25,8 +25,9 @@ def _lib():
 
 def test_header_declares_expected_entry_points():
     assert _declared() == sorted([
-        "la_abi_version", "la_status_string", "la_based_parallel_fwd", "la_based_chunked_workspace_bytes",
-        "la_based_chunked_fwd", "la_sliding_window_fwd", "la_taylor_feature_map"])
+        "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
+        "la_based_chunked_workspace_bytes", "la_based_chunked_fwd", "la_sliding_window_fwd",
+        "la_taylor_feature_map"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -37,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib()
-    assert lib.la_abi_version() == 1
+    assert lib.la_abi_version() == 2
     for code in range(-8, 1):
         s = lib.la_status_string(code).decode()
         assert s and s != "unknown status"
@@ -54,13 +55,14 @@ P = ctypes.c_void_p(16)   # dummy non-null, 16-byte aligned pointer; never deref
 def test_parallel_argument_errors():
     lib = _lib()
     f = lib.la_based_parallel_fwd
+    need = lib.la_based_parallel_workspace_bytes(1, 1, 8, 16, 64, 1)
     ok_args = dict(q=P, k=P, v=P, dt=1, out=P, odt=1, den=None, B=1, H=1, N=8, d=16, dv=64, scale=0.25, eps=1e-6,
-                   norm=1)
+                   norm=1, ws=P, ws_bytes=need)
 
     def call(**kw):
         a = dict(ok_args, **kw)
         return f(a["q"], a["k"], a["v"], a["dt"], a["out"], a["odt"], a["den"], a["B"], a["H"], a["N"], a["d"],
-                 a["dv"], a["scale"], a["eps"], a["norm"], None)
+                 a["dv"], a["scale"], a["eps"], a["norm"], a["ws"], a["ws_bytes"], None)
 
     assert call(q=None) == -1
     assert call(d=0) == -2
@@ -73,8 +75,25 @@ def test_parallel_argument_errors():
     assert call(d=129) == -5
     assert call(dv=200) == -5
     assert call(q=ctypes.c_void_p(17)) == -8
+    assert call(ws=None) == -6                 # bf16, d = 16, dv = 64 needs the V^T workspace
+    assert call(ws_bytes=need - 1) == -6
+    assert call(ws=ctypes.c_void_p(24)) == -8
     assert call(N=0) == 0          # empty: nothing to launch
     assert call(B=0) == 0
+
+
+def test_parallel_workspace_sizes():
+    lib = _lib()
+    ws = lib.la_based_parallel_workspace_bytes
+    # per (b, h) and 64-key block: fp16 V^T (dv rows padded to 68 keys, whole 1 KB units) and
+    # the fp32 column sums of V
+    assert ws(2, 16, 8192, 16, 64, 1) == 32 * 128 * (9216 + 256)
+    assert ws(1, 1, 65, 16, 32, 1) == 2 * (5120 + 128)
+    assert ws(1, 1, 64, 16, 64, 0) == 0        # fp32 inputs: no workspace
+    assert ws(1, 1, 64, 32, 64, 1) == 0        # d != 16
+    assert ws(1, 1, 64, 16, 60, 1) == 0        # dv % 8 != 0
+    assert ws(1, 1, 64, 16, 72, 1) == 0        # dv > 64
+    assert ws(0, 1, 64, 16, 64, 1) == 0
 
 
 def test_sliding_argument_errors():

@@ -10,12 +10,13 @@
 // (benchmarks/chunked_attention_benchmark.py:34-53) evaluated through the exact identity
 // phi(q).phi(k) = 1 + s + s^2/2, so phi is never materialised.
 //
-// Precision.  The P.V product runs as an fp16 MFMA: V is converted bf16 -> fp16 while it is
-// staged (exact for 2^-14 <= |v| <= 65504) and u is rounded to fp16 (2^-11 relative, 8x finer
-// than bf16).  Q is pre-scaled by 2^-k (exact) so that the rounded quantity is u * 2^-2k ~ r
-// and stays far from fp16 overflow (|q.k| * scale < ~255).  The constant 1 of p is kept exact:
-//   * key blocks strictly before the work-group's queries contribute sum(v) through an fp32
-//     running column sum of V (v_dot2 against packed ones), snapshotted per wave;
+// Precision.  The P.V product runs as an fp16 MFMA: V is converted bf16 -> fp16 (exact for
+// 2^-14 <= |v| <= 65504) and u is rounded to fp16 (2^-11 relative, 8x finer than bf16).  Q is
+// pre-scaled by 2^-k (exact) so that the rounded quantity is u * 2^-2k ~ r and stays far from
+// fp16 overflow (|q.k| * scale < ~255).  The constant 1 of p is kept exact:
+//   * key blocks strictly before the wave's queries contribute sum(v) through fp32 column sums
+//     of V: computed by the pre-pass and prefix-summed over blocks (packed path), or kept as a
+//     running sum in the key loop (v_dot2 against packed ones) and snapshotted per wave;
 //   * the wave's own diagonal block adds its causal "ones" through a second MFMA whose B
 //     operand is the causal mask times the weight of "1" in u units (split hi + lo in fp16;
 //     exact for scale = 1/sqrt(d)).
@@ -24,10 +25,19 @@
 //
 // Tiling.  4 waves per work-group; each wave owns 32*QT queries (QT 32x32 N-tiles) and the
 // full dv (MT 32-row M-tiles of the transposed output O^T = V^T P^T).  Keys stream through LDS
-// in blocks of 64 (double buffered): K row-major [key][d], V transposed [dv][key] so both
-// MFMA operands are contiguous 8-byte / 16-byte LDS reads.  Scores are computed transposed,
+// in blocks of 64: K row-major [key][d], V transposed [dv][key] in fp16 (rows padded to VROW)
+// so both MFMA operands are contiguous LDS reads.  Scores are computed transposed,
 // S^T = K Q^T, so the score accumulator layout is directly the B operand layout of the PV
 // MFMA (no cross-lane shuffles).
+//
+// Staging, packed path (d = 16, dv % 8 == 0, dv <= 64, bf16): a pre-pass (vt_pack_kernel)
+// writes V once as fp16 V^T blocks in exactly the LDS layout into a caller workspace, with the
+// per-block column sums of V (prefix-summed by colsum_scan_kernel).  The
+// main kernel then copies K rows and V^T blocks global -> LDS with buffer_load ... lds (no
+// staging registers, no conversion; K rows past N read as zero) into NRAW stages, NRAW - 2
+// blocks ahead, and synchronises the work-group once per two blocks.  Barriers are plain
+// s_barrier with explicit vmcnt / lgkmcnt waits so that in-flight copies are not drained.
+// Other shapes stage K and V through registers into a double-buffered LDS block.
 #include "la_common.hpp"
 #include "la_internal.hpp"
 #include "la_stage.hpp"
@@ -40,36 +50,152 @@ struct ParallelParams {
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
+  const uint16_t* vt;     // packed fp16 V^T blocks (packed path), [BH][nb64][vt_block]
+  const float* vpre;      // packed path: exclusive prefix over blocks of the column sums of V, [BH][nb64][DV]
   void* out;
   float* den;
-  int BH, N, d, dv, nqb;
+  int BH, N, d, dv, nqb, nb64;
   float inv_c, inv_c2, fscale, eps;
   float qscale;           // 2^-k applied to q (exact in bf16)
   u32 ones_hi, ones_lo;   // fp16 bits of the weight W of "1" in u units, hi + lo (both halves)
   int normalize, out_f32;
 };
 
+constexpr int NRAW = 7;   // LDS stages of the packed path
+
+// Packed V^T block: DV rows of VROW fp16 (keys 0..63 + padding), rounded up to whole 1 KB
+// copy units.
+template <int DV>
+struct VtBlock {
+  static constexpr int units = (DV * VROW * 2 + 1023) / 1024;
+  static constexpr int bytes = units * 1024;
+};
+
+size_t vt_block_bytes(int dv) { return dv <= 32 ? (size_t)VtBlock<32>::bytes : (size_t)VtBlock<64>::bytes; }
+
+bool packed_shape(int d, int dv) { return d == 16 && dv % 8 == 0 && dv <= 64; }
+
+// V (bf16 [N][dv]) of one head -> fp16 V^T blocks [nb64][DV][VROW], zero for keys >= N,
+// rows >= dv and the padding.
+// Also writes the column sums of the block, colsum[bh][blk][DV].
+template <int DV>
+__global__ __launch_bounds__(256) void vt_pack_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt,
+                                                      float* __restrict__ colsum, int N, int dv, int nb64) {
+  constexpr int NP = 256 / DV;   // partial sums per column
+  __shared__ float tile[BN][DV + 1];
+  __shared__ float part[NP][DV];
+  const int blk = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
+  const int row0 = blk * BN;
+  const uint16_t* __restrict__ src = v + ((size_t)bh * N + row0) * dv;
+  constexpr int NLD = BN * (DV / 2) / 256;   // bf16 pairs per thread
+  u32 x[NLD];
+#pragma unroll
+  for (int i = 0; i < NLD; ++i) {   // all loads in flight before the first LDS store
+    const int idx = tid + 256 * i, key = idx / (DV / 2), col = 2 * (idx % (DV / 2));
+    x[i] = (row0 + key < N && col < dv) ? *reinterpret_cast<const u32*>(src + (size_t)key * dv + col) : 0u;
+  }
+#pragma unroll
+  for (int i = 0; i < NLD; ++i) {
+    const int idx = tid + 256 * i, key = idx / (DV / 2), col = 2 * (idx % (DV / 2));
+    tile[key][col] = bf16_lo_to_f32(x[i]);
+    tile[key][col + 1] = bf16_hi_to_f32(x[i]);
+  }
+  __syncthreads();
+  u32* __restrict__ dst = reinterpret_cast<u32*>(vt + ((size_t)bh * nb64 + blk) * (VtBlock<DV>::bytes / 2));
+  for (int idx = tid; idx < VtBlock<DV>::bytes / 4; idx += 256) {
+    const int row = (2 * idx) / VROW, col = (2 * idx) % VROW;
+    u32 y = 0u;
+    if (row < DV && col < BN) y = pack_f16x2(tile[col][row], tile[col + 1][row]);
+    dst[idx] = y;
+  }
+  {
+    const int col = tid % DV, pi = tid / DV;
+    float t = 0.f;
+#pragma unroll
+    for (int key = pi * (BN / NP); key < (pi + 1) * (BN / NP); ++key) t += tile[key][col];
+    part[pi][col] = t;
+  }
+  __syncthreads();
+  if (tid < DV) {
+    float t = 0.f;
+#pragma unroll
+    for (int pi = 0; pi < NP; ++pi) t += part[pi][tid];
+    colsum[((size_t)bh * nb64 + blk) * DV + tid] = t;
+  }
+}
+
+// colsum[bh][blk][DV] -> exclusive prefix over blk, in place.  One work-group per head; the
+// head's column sums go through LDS in tiles of 4096 values (all loads of a tile in flight at
+// once), NQ threads per column scan a tile, and a carry links the tiles.
+template <int DV>
+__global__ __launch_bounds__(256) void colsum_scan_kernel(float* __restrict__ colsum, int nb64) {
+  constexpr int TB = 4096 / DV;   // blocks per tile
+  constexpr int NQ = 256 / DV;    // threads per column
+  constexpr int PER = TB / NQ;    // blocks per thread and tile
+  __shared__ float tile[TB * DV];
+  __shared__ float tot[NQ][DV];
+  const int tid = threadIdx.x, col = tid % DV, qi = tid / DV;
+  float* __restrict__ c = colsum + (size_t)blockIdx.x * nb64 * DV;
+  float carry = 0.f;
+  for (int t0 = 0; t0 < nb64; t0 += TB) {
+    const int nt = min(TB, nb64 - t0);
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {   // all loads in flight before the first LDS store
+      const int idx = tid + 256 * i;
+      x[i] = idx < nt * DV ? c[(size_t)t0 * DV + idx] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) tile[tid + 256 * i] = x[i];
+    __syncthreads();
+    float part = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int bl = qi * PER + i;
+      if (bl < nt) part += tile[bl * DV + col];
+    }
+    tot[qi][col] = part;
+    __syncthreads();
+    float run = carry, all = carry;
+#pragma unroll
+    for (int q2 = 0; q2 < NQ; ++q2) {
+      if (q2 < qi) run += tot[q2][col];
+      all += tot[q2][col];
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int bl = qi * PER + i;
+      if (bl < nt) {
+        const float x = tile[bl * DV + col];
+        tile[bl * DV + col] = run;
+        run += x;
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < nt * DV; idx += 256) c[(size_t)t0 * DV + idx] = tile[idx];
+    carry = all;
+    __syncthreads();
+  }
+}
+
 // UNIT: 1/c scales to exactly 1 (scale = 1/sqrt(d) with d a power of 4), so the score MFMA
 // starts from the inline constant 1.0 and u = b*b - 1.
-//
-// DMA (d = 16, dv % 8 == 0): K and V blocks are copied global -> LDS by buffer_load ... lds
-// (no staging registers, out-of-range rows read as zero) three blocks ahead into four raw
-// stages; V is converted to fp16 and transposed LDS -> LDS one block ahead.  Barriers are
-// plain s_barrier with explicit vmcnt / lgkmcnt waits so that in-flight copies are not drained.
-template <int KS, int MT, int QT, bool VEC, bool UNIT, bool DMA, class KsT, class VTsT, class SnapT, class KrawT,
-          class VrawT>
-__device__ __forceinline__ void based_parallel_body(const ParallelParams& p, KsT* __restrict__ Ks,
-                                                    VTsT* __restrict__ VTs, SnapT* __restrict__ snap,
-                                                    KrawT* __restrict__ Kraw, VrawT* __restrict__ Vraw) {
+template <int KS, int MT, int QT, bool VEC, bool UNIT, bool PACKED>
+__global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const ParallelParams p) {
   constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128 * QT, NSNAP = BM / BN;
   constexpr int KROW = DK + 8;
   constexpr int LPR = 256 / DV;      // threads per V^T row in the running column sum
   constexpr int KPL = BN / LPR;      // keys per thread in the running column sum
   using Stager = BlockStager<KS, MT, VEC, true>;
-  static_assert(!DMA || KS == 1, "DMA staging is for d = 16");
-  constexpr int NRAW = 4;                 // raw DMA stages
-  constexpr int NKU = 2, NVU = DV / 8;    // 1 KB DMA units per block (K, V)
-  constexpr int NU = NKU + NVU;
+  static_assert(!PACKED || KS == 1, "the packed path is for d = 16");
+  constexpr int NVU = VtBlock<DV>::units;
+  constexpr int NU = 2 + NVU;                       // 1 KB copy units per block: K (2), V^T
+  constexpr int STAGE = 1024 + NVU * 512;           // halves per packed stage: K, then V^T
+
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[PACKED ? 1 : 2][PACKED ? 8 : BN * KROW];
+  __shared__ __attribute__((aligned(16))) uint16_t VTs[PACKED ? 1 : 2][PACKED ? 8 : DV * VROW];
+  __shared__ __attribute__((aligned(16))) uint16_t stage[PACKED ? NRAW : 1][PACKED ? STAGE : 8];
+  __shared__ __attribute__((aligned(16))) float snap[PACKED ? 1 : NSNAP][PACKED ? 4 : DV * LPR];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
@@ -130,92 +256,145 @@ __device__ __forceinline__ void based_parallel_body(const ParallelParams& p, KsT
 
   const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
 
-  // ---- DMA staging helpers
+  // ---- packed path: global -> LDS copies.  Wave wu owns units wu, wu + 4, wu + 8 of every
+  // block; unit u lands at byte 1024 u of the stage (K units 0-1, V^T units 2..).
   const int wu = __builtin_amdgcn_readfirstlane(w);
   const int my_units = NU / 4 + (wu < NU % 4 ? 1 : 0);
+  constexpr int VTB = VtBlock<DV>::bytes;
   const u32x4 rk = buffer_rsrc(kg, (u32)N * 32u);
-  const u32x4 rv = buffer_rsrc(vg, (u32)N * (u32)dv * 2u);
-  auto issue_dma = [&](int blk) {
-    const int st = blk & (NRAW - 1);
-    const int row0 = blk * BN;
+  const u32x4 rv = buffer_rsrc(p.vt + (size_t)bh * p.nb64 * (VTB / 2), (u32)p.nb64 * (u32)VTB);
+  int uoff[3];
 #pragma unroll
-    for (int i = 0; i < (NU + 3) / 4; ++i) {
+  for (int i = 0; i < 3; ++i) {
+    const int u = wu + 4 * i;
+    if (u < 2) {
+      // K slot sl = 2 key + (c ^ ((key >> 2) & 1)) holds 16-byte chunk c of the key's row
+      const int sl = 64 * u + lane, key = sl >> 1, c = (sl & 1) ^ ((key >> 2) & 1);
+      uoff[i] = key * 32 + 16 * c;
+    } else {
+      uoff[i] = 1024 * (u - 2) + 16 * lane;
+    }
+  }
+  auto issue = [&](int blk) {
+    const u32 base = lds_addr(&stage[blk % NRAW][0]);
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
       const int u = wu + 4 * i;
       if (u >= NU) break;
-      if (u < NKU) {
-        // K slot sl = 2 key + (c ^ ((key >> 2) & 1)): 16-byte chunk c of key row, swizzled
-        const int sl = 64 * u + lane, key = sl >> 1, c = (sl & 1) ^ ((key >> 2) & 1);
-        lds_copy16(rk, lds_addr(&Kraw[st][512 * u]), ((row0 + key) * 16 + 8 * c) * 2);
-      } else {
-        const int ch = 64 * (u - NKU) + lane, key = ch / (DV / 8), col = 8 * (ch % (DV / 8));
-        const int off = col < dv ? ((row0 + key) * dv + col) * 2 : 0x7ffffff0;
-        lds_copy16(rv, lds_addr(&Vraw[st][512 * (u - NKU)]), off);
-      }
+      if (u < 2)
+        lds_copy16(rk, base + 1024 * u, uoff[i] + blk * (BN * 32));
+      else
+        lds_copy16(rv, base + 1024 * u, uoff[i] + blk * VTB);
     }
   };
-  // raw V of block blk (bf16 [key][DV]) -> VTs[blk & 1] (fp16 [dv][key])
-  auto convert_v = [&](int blk) {
-    const uint16_t* src = &Vraw[blk & (NRAW - 1)][0];
-    uint16_t* dstb = &VTs[blk & 1][0];
-#pragma unroll
-    for (int g = tid; g < (DV / 4) * (BN / 4); g += 256) {
-      const int g4 = g % (DV / 4), kg4 = g / (DV / 4);
-      u32x2 x[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x[i] = *reinterpret_cast<const u32x2*>(&src[(4 * kg4 + i) * DV + 4 * g4]);
-      const u32 a0 = x[0][0], a1 = x[1][0], a2 = x[2][0], a3 = x[3][0];
-      const u32 b0 = x[0][1], b1 = x[1][1], b2 = x[2][1], b3 = x[3][1];
-      uint16_t* dst = dstb + (4 * g4) * VROW + 4 * kg4;
-      *reinterpret_cast<u32x2*>(dst) = (u32x2){pack_f16x2(bf16_lo_to_f32(a0), bf16_lo_to_f32(a1)),
-                                               pack_f16x2(bf16_lo_to_f32(a2), bf16_lo_to_f32(a3))};
-      *reinterpret_cast<u32x2*>(dst + VROW) = (u32x2){pack_f16x2(bf16_hi_to_f32(a0), bf16_hi_to_f32(a1)),
-                                                      pack_f16x2(bf16_hi_to_f32(a2), bf16_hi_to_f32(a3))};
-      *reinterpret_cast<u32x2*>(dst + 2 * VROW) = (u32x2){pack_f16x2(bf16_lo_to_f32(b0), bf16_lo_to_f32(b1)),
-                                                          pack_f16x2(bf16_lo_to_f32(b2), bf16_lo_to_f32(b3))};
-      *reinterpret_cast<u32x2*>(dst + 3 * VROW) = (u32x2){pack_f16x2(bf16_hi_to_f32(b0), bf16_hi_to_f32(b1)),
-                                                          pack_f16x2(bf16_hi_to_f32(b2), bf16_hi_to_f32(b3))};
-    }
-  };
-  // LDS-only barrier: my LDS writes done, then s_barrier; the asm clobbers keep the compiler
-  // from moving memory operations across it.
+  // LDS-only barrier: this wave's LDS operations done, then s_barrier; the empty asm
+  // statements keep the compiler from moving memory operations across it.
   auto lds_barrier = [&]() {
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0), vmcnt/expcnt unchanged
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0), vmcnt / expcnt unchanged
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  // wait until at most `left` DMA units of this wave are still in flight
-  auto wait_dma = [&](int left) {
+  // wait until at most `left` copies of this wave are in flight (s_waitcnt vmcnt(left); a
+  // count above 12 waits for 12)
+  auto wait_copies = [&](int left) {
     asm volatile("" ::: "memory");
-    if (left >= 6) __builtin_amdgcn_s_waitcnt(0x0f76);
-    else if (left == 5) __builtin_amdgcn_s_waitcnt(0x0f75);
-    else if (left == 4) __builtin_amdgcn_s_waitcnt(0x0f74);
-    else if (left == 3) __builtin_amdgcn_s_waitcnt(0x0f73);
-    else if (left == 2) __builtin_amdgcn_s_waitcnt(0x0f72);
-    else if (left == 1) __builtin_amdgcn_s_waitcnt(0x0f71);
-    else __builtin_amdgcn_s_waitcnt(0x0f70);
+    switch (left) {
+      case 0: __builtin_amdgcn_s_waitcnt(0x0f70); break;
+      case 1: __builtin_amdgcn_s_waitcnt(0x0f71); break;
+      case 2: __builtin_amdgcn_s_waitcnt(0x0f72); break;
+      case 3: __builtin_amdgcn_s_waitcnt(0x0f73); break;
+      case 4: __builtin_amdgcn_s_waitcnt(0x0f74); break;
+      case 5: __builtin_amdgcn_s_waitcnt(0x0f75); break;
+      case 6: __builtin_amdgcn_s_waitcnt(0x0f76); break;
+      case 7: __builtin_amdgcn_s_waitcnt(0x0f77); break;
+      case 8: __builtin_amdgcn_s_waitcnt(0x0f78); break;
+      case 9: __builtin_amdgcn_s_waitcnt(0x0f79); break;
+      case 10: __builtin_amdgcn_s_waitcnt(0x0f7a); break;
+      case 11: __builtin_amdgcn_s_waitcnt(0x0f7b); break;
+      default: __builtin_amdgcn_s_waitcnt(0x0f7c); break;
+    }
     asm volatile("" ::: "memory");
   };
+  // K fragment (A operand of the score MFMA): key 32 ks + n, dims 16 kk + 8 h .. +7
   auto kfrag = [&](int j, int ks, int kk) -> u32x4 {
-    if (DMA) {
-      const int key = 32 * ks + n;
+    const int key = 32 * ks + n;
+    if (PACKED) {
       const int sl = 2 * key + (h ^ ((key >> 2) & 1));
-      return *reinterpret_cast<const u32x4*>(&Kraw[j & (NRAW - 1)][8 * sl]);
+      return *reinterpret_cast<const u32x4*>(&stage[j % NRAW][8 * sl]);
     }
-    return *reinterpret_cast<const u32x4*>(&Ks[j & 1][(32 * ks + n) * KROW + 16 * kk + 8 * h]);
+    return *reinterpret_cast<const u32x4*>(&Ks[j & 1][key * KROW + 16 * kk + 8 * h]);
+  };
+  // fp16 V^T of block j, [DV][VROW]
+  auto vtile = [&](int j) -> const uint16_t* { return PACKED ? &stage[j % NRAW][1024] : &VTs[j & 1][0]; };
+
+  // Full-block pieces.  scores: b = K Q^T + 1/c for the two 32-key halves of block j;
+  // elementwise: u = b*b - 1/c^2 rounded to fp16 (the PV B operand) and its row sums;
+  // pv: acc += V^T u^T.
+  auto scores = [&](int j, f32x16 (&b)[2][QT]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4 kf[KS];
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) kf[kk] = kfrag(j, ks, kk);
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        b[ks][qt] = splat16(inv_c);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) b[ks][qt] = mfma32x32x16(kf[kk], qf[qt][kk], b[ks][qt]);
+      }
+    }
+  };
+  auto elementwise = [&](const f32x16 (&b)[2][QT], u32x4 (&pf)[2][QT][2]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        float r = rsum[qt];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          u32 wv[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const int i = 8 * m + 2 * c;
+            const float x0 = b[ks][qt][i], x1 = b[ks][qt][i + 1];
+            wv[c] = pack_f16x2(__builtin_fmaf(x0, x0, -inv_c2), __builtin_fmaf(x1, x1, -inv_c2));
+            r = dot2_f16(wv[c], kOnes, r);
+          }
+          pf[ks][qt][m] = (u32x4){wv[0], wv[1], wv[2], wv[3]};
+        }
+        rsum[qt] = r;
+      }
+  };
+  auto pv = [&](int j, const u32x4 (&pf)[2][QT][2]) {
+    const uint16_t* vt = vtile(j);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const uint16_t* vp = vt + (32 * mt + n) * VROW + 32 * ks + 16 * m + 4 * h;
+          const u32x2 a0 = *reinterpret_cast<const u32x2*>(vp);
+          const u32x2 a1 = *reinterpret_cast<const u32x2*>(vp + 8);
+          const u32x4 vf = {a0[0], a0[1], a1[0], a1[1]};
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) acc[qt][mt] = mfma32x32x16_f16(vf, pf[ks][qt][m], acc[qt][mt]);
+        }
   };
 
   Stager st;
-  if (DMA) {
-    // drain the Q loads so only DMA units are counted by vmcnt from here on
+  if (PACKED) {
+    // drain the Q loads so that vmcnt counts only copies from here on
     __builtin_amdgcn_s_waitcnt(0x0f70);
-    issue_dma(0);
-    if (nblk > 1) issue_dma(1);
-    if (nblk > 2) issue_dma(2);
-    wait_dma(my_units * ((nblk > 2) ? 2 : (nblk > 1 ? 1 : 0)));
+    const int issued = min(NRAW - 3, nblk - 1);
+#pragma unroll
+    for (int b = 0; b <= NRAW - 3; ++b)
+      if (b <= issued) issue(b);
+    wait_copies(my_units * (issued - min(1, nblk - 1)));   // blocks 0 and 1 landed
     lds_barrier();
-    convert_v(0);
-    if (jb0 == 0) snap[0][tid] = 0.f;
+    if (NRAW - 2 < nblk) issue(NRAW - 2);
+    if (NRAW - 1 < nblk) issue(NRAW - 1);
   } else {
     st.load(kg, vg, 0, N, d, dv, tid);
     st.store(Ks[0], VTs[0], tid);
@@ -223,20 +402,11 @@ __device__ __forceinline__ void based_parallel_body(const ParallelParams& p, KsT
     __syncthreads();
   }
 
-  for (int j = 0; j < nblk; ++j) {
-    const int s = j & 1;
-    if (DMA) {
-      // block j+1 must have landed; blocks j+2 (and j+3 once issued) may still be in flight
-      wait_dma(j + 2 < nblk ? my_units : 0);
-      lds_barrier();
-      if (j + 3 < nblk) issue_dma(j + 3);
-      if (j + 1 < nblk) convert_v(j + 1);
-    } else {
-      if (j + 1 < nblk) st.load(kg, vg, (j + 1) * BN, N, d, dv, tid);
-    }
-
-    if (j <= jb0 + NSNAP - 2) {
-      const uint16_t* src = &VTs[s][vs_row * VROW + vs_seg * KPL];
+  // One key block of the loop.
+  auto block_step = [&](int j) {
+    if (!PACKED && j <= jb0 + NSNAP - 2) {
+      const uint16_t* vt = vtile(j);
+      const uint16_t* src = vt + vs_row * VROW + vs_seg * KPL;
 #pragma unroll
       for (int e = 0; e < KPL; e += 4) {
         const u32x2 x = *reinterpret_cast<const u32x2*>(src + e);
@@ -249,49 +419,15 @@ __device__ __forceinline__ void based_parallel_body(const ParallelParams& p, KsT
 
     if (wave_live && j < jd) {
       // Full block: every key precedes every query of this wave -- no mask, no "1" term
-      // (the running column sum covers it).  All score MFMAs first, then the P.V MFMAs.
+      // (the running column sum covers it).
+      f32x16 b[2][QT];
       u32x4 pf[2][QT][2];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        u32x4 kf[KS];
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) kf[kk] = kfrag(j, ks, kk);
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          f32x16 b = splat16(inv_c);
-#pragma unroll
-          for (int kk = 0; kk < KS; ++kk) b = mfma32x32x16(kf[kk], qf[qt][kk], b);
-          float r = rsum[qt];
-#pragma unroll
-          for (int m = 0; m < 2; ++m) {
-            u32 w[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const int i = 8 * m + 2 * c;
-              w[c] = pack_f16x2(__builtin_fmaf(b[i], b[i], -inv_c2), __builtin_fmaf(b[i + 1], b[i + 1], -inv_c2));
-              r = dot2_f16(w[c], kOnes, r);
-            }
-            pf[ks][qt][m] = (u32x4){w[0], w[1], w[2], w[3]};
-          }
-          rsum[qt] = r;
-        }
-      }
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int m = 0; m < 2; ++m) {
-            const uint16_t* vp = &VTs[s][(32 * mt + n) * VROW + 32 * ks + 16 * m + 4 * h];
-            const u32x2 a0 = *reinterpret_cast<const u32x2*>(vp);
-            const u32x2 a1 = *reinterpret_cast<const u32x2*>(vp + 8);
-            const u32x4 vf = {a0[0], a0[1], a1[0], a1[1]};
-#pragma unroll
-            for (int qt = 0; qt < QT; ++qt) acc[qt][mt] = mfma32x32x16_f16(vf, pf[ks][qt][m], acc[qt][mt]);
-          }
+      scores(j, b);
+      elementwise(b, pf);
+      pv(j, pf);
     } else if (wave_live && j == jd) {
       // Diagonal block: causal mask on u, plus the exact "1" of p through a mask MFMA.
-      constexpr bool diag_block = true;
+      const uint16_t* vt = vtile(j);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int kb = j * BN + 32 * ks;
@@ -331,22 +467,20 @@ __device__ __forceinline__ void based_parallel_body(const ParallelParams& p, KsT
             r = dot2_f16(pf[qt][m][3], kOnes, r);
             rsum[qt] = r;
           }
-          if (diag_block) {
-            // causal mask times W for the exact "1" of p; element e <-> key
-            // kb + 16m + 8(e/4) + 4h + (e%4)
+          // causal mask times W for the exact "1" of p; element e <-> key
+          // kb + 16m + 8(e/4) + 4h + (e%4)
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
-              u32 wd[4];
+          for (int m = 0; m < 2; ++m) {
+            u32 wd[4];
 #pragma unroll
-              for (int e2 = 0; e2 < 4; ++e2) {
-                const int e = 2 * e2;
-                const int key0 = kb + 16 * m + 8 * (e >> 2) + 4 * h + (e & 3);
-                const u32 lo = (key0 <= query) ? (p.ones_hi & 0xffffu) : 0u;
-                const u32 hi = (key0 + 1 <= query) ? (p.ones_hi & 0xffff0000u) : 0u;
-                wd[e2] = lo | hi;
-              }
-              mk[qt][m] = (u32x4){wd[0], wd[1], wd[2], wd[3]};
+            for (int e2 = 0; e2 < 4; ++e2) {
+              const int e = 2 * e2;
+              const int key0 = kb + 16 * m + 8 * (e >> 2) + 4 * h + (e & 3);
+              const u32 lo = (key0 <= query) ? (p.ones_hi & 0xffffu) : 0u;
+              const u32 hi = (key0 + 1 <= query) ? (p.ones_hi & 0xffff0000u) : 0u;
+              wd[e2] = lo | hi;
             }
+            mk[qt][m] = (u32x4){wd[0], wd[1], wd[2], wd[3]};
           }
         }
 
@@ -354,7 +488,7 @@ __device__ __forceinline__ void based_parallel_body(const ParallelParams& p, KsT
         for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
           for (int m = 0; m < 2; ++m) {
-            const uint16_t* vp = &VTs[s][(32 * mt + n) * VROW + 32 * ks + 16 * m + 4 * h];
+            const uint16_t* vp = vt + (32 * mt + n) * VROW + 32 * ks + 16 * m + 4 * h;
             const u32x2 a0 = *reinterpret_cast<const u32x2*>(vp);
             const u32x2 a1 = *reinterpret_cast<const u32x2*>(vp + 8);
             const u32x4 vf = {a0[0], a0[1], a1[0], a1[1]};
@@ -362,36 +496,53 @@ __device__ __forceinline__ void based_parallel_body(const ParallelParams& p, KsT
             for (int qt = 0; qt < QT; ++qt) {
               if (!act[qt]) continue;
               acc[qt][mt] = mfma32x32x16_f16(vf, pf[qt][m], acc[qt][mt]);
-              if (diag_block) {
-                acc[qt][mt] = mfma32x32x16_f16(vf, mk[qt][m], acc[qt][mt]);
-                if (p.ones_lo != 0u) {
-                  // same mask pattern, low part of 2/c^2
-                  u32x4 ml;
+              acc[qt][mt] = mfma32x32x16_f16(vf, mk[qt][m], acc[qt][mt]);
+              if (p.ones_lo != 0u) {
+                // same mask pattern, low part of W
+                u32x4 ml;
 #pragma unroll
-                  for (int t = 0; t < 4; ++t) {
-                    const u32 wv = mk[qt][m][t];
-                    ml[t] = ((wv & 0xffffu) ? (p.ones_lo & 0xffffu) : 0u) |
-                            ((wv & 0xffff0000u) ? (p.ones_lo & 0xffff0000u) : 0u);
-                  }
-                  acc[qt][mt] = mfma32x32x16_f16(vf, ml, acc[qt][mt]);
+                for (int t = 0; t < 4; ++t) {
+                  const u32 wv = mk[qt][m][t];
+                  ml[t] = ((wv & 0xffffu) ? (p.ones_lo & 0xffffu) : 0u) |
+                          ((wv & 0xffff0000u) ? (p.ones_lo & 0xffff0000u) : 0u);
                 }
+                acc[qt][mt] = mfma32x32x16_f16(vf, ml, acc[qt][mt]);
               }
             }
           }
         }
       }
     }
+  };
 
-    if (!DMA) {
-      if (j + 1 < nblk) st.store(Ks[s ^ 1], VTs[s ^ 1], tid);
+  if (PACKED) {
+    for (int j = 0; j < nblk; j += 2) {
+      if (j >= 2) {
+        // iterations j and j+1 read blocks j and j+1; stages of blocks j-2 and j-1 are free
+        // after the barrier
+        const int issued = min(j + NRAW - 3, nblk - 1);
+        wait_copies(my_units * max(0, issued - min(j + 1, nblk - 1)));
+        lds_barrier();
+        if (j + NRAW - 2 < nblk) issue(j + NRAW - 2);
+        if (j + NRAW - 1 < nblk) issue(j + NRAW - 1);
+      }
+      block_step(j);
+      if (j + 1 < nblk) block_step(j + 1);
+    }
+    lds_barrier();
+  } else {
+    for (int j = 0; j < nblk; ++j) {
+      if (j + 1 < nblk) st.load(kg, vg, (j + 1) * BN, N, d, dv, tid);
+      block_step(j);
+      if (j + 1 < nblk) st.store(Ks[(j & 1) ^ 1], VTs[(j & 1) ^ 1], tid);
       __syncthreads();
     }
   }
-  if (DMA) lds_barrier();   // snapshots written in the last iterations
 
   if (!wave_live) return;
 
-  // epilogue: num = acc/W + vsum, den = (t+1) + rowsum/W  (fscale = 1/W)
+  // epilogue: num = acc/W + vsum, den = (t+1) + rowsum/W  (fscale = 1/W); vsum = column sums of
+  // V over the keys before this wave's diagonal block
   const int si = jd - jb0;
   float vsum[MT][16];
 #pragma unroll
@@ -400,8 +551,12 @@ __device__ __forceinline__ void based_parallel_body(const ParallelParams& p, KsT
     for (int i = 0; i < 16; ++i) {
       const int row = 32 * mt + c32_row(i, h);
       float t = 0.f;
+      if (PACKED) {
+        t = p.vpre[((size_t)bh * p.nb64 + jd) * DV + row];
+      } else {
 #pragma unroll
-      for (int sg = 0; sg < LPR; ++sg) t += snap[si][row * LPR + sg];
+        for (int sg = 0; sg < LPR; ++sg) t += snap[si][row * LPR + sg];
+      }
       vsum[mt][i] = t;
     }
 
@@ -448,36 +603,24 @@ __device__ __forceinline__ void based_parallel_body(const ParallelParams& p, KsT
   }
 }
 
-template <int KS, int MT, int QT, bool VEC, bool UNIT, bool DMA>
-__global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const ParallelParams p) {
-  constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128 * QT, NSNAP = BM / BN;
-  constexpr int KROW = DK + 8;
-  constexpr int LPR = 256 / DV;
-  constexpr int NRAW = 4;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[DMA ? 1 : 2][DMA ? 8 : BN * KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t VTs[2][DV * VROW];
-  __shared__ __attribute__((aligned(16))) float snap[NSNAP][DV * LPR];
-  __shared__ __attribute__((aligned(16))) uint16_t Kraw[DMA ? NRAW : 1][DMA ? BN * 16 : 8];
-  __shared__ __attribute__((aligned(16))) uint16_t Vraw[DMA ? NRAW : 1][DMA ? BN * DV : 8];
-  based_parallel_body<KS, MT, QT, VEC, UNIT, DMA>(p, Ks, VTs, snap, Kraw, Vraw);
-}
-
 template <int KS, int MT, int QT>
-int launch_bf16(const ParallelParams& pp, bool vec, hipStream_t stream) {
+int launch_bf16(const ParallelParams& pp, bool vec, bool packed, hipStream_t stream) {
   constexpr int BM = 128 * QT;
   ParallelParams p = pp;
   p.nqb = (p.N + BM - 1) / BM;
   const dim3 grid((unsigned)(p.nqb * p.BH)), block(256);
   const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
-  // buffer offsets are 32-bit: one head's K and V must stay below 2^31 bytes
-  const bool dma = vec && p.d == 16 && (p.dv % 8) == 0 && (long long)p.N * p.dv * 2 < (1ll << 30);
   if constexpr (KS == 1 && MT <= 2) {
-    if (dma && unit) {
-      hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, true, true>), grid, block, 0, stream, p);
-      return (int)hipGetLastError();
-    }
-    if (dma) {
-      hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, false, true>), grid, block, 0, stream, p);
+    if (packed) {
+      constexpr int DV = 32 * MT;
+      hipLaunchKernelGGL((vt_pack_kernel<DV>), dim3((unsigned)p.nb64, (unsigned)p.BH), dim3(256), 0, stream, p.v,
+                         const_cast<uint16_t*>(p.vt), const_cast<float*>(p.vpre), p.N, p.dv, p.nb64);
+      hipLaunchKernelGGL((colsum_scan_kernel<DV>), dim3((unsigned)p.BH), dim3(256), 0, stream,
+                         const_cast<float*>(p.vpre), p.nb64);
+      if (unit)
+        hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, true, true>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, false, true>), grid, block, 0, stream, p);
       return (int)hipGetLastError();
     }
   }
@@ -491,14 +634,22 @@ int launch_bf16(const ParallelParams& pp, bool vec, hipStream_t stream) {
 }
 
 template <int KS>
-int dispatch_mt(const ParallelParams& p, bool vec, hipStream_t stream) {
+int dispatch_mt(const ParallelParams& p, bool vec, bool packed, hipStream_t stream) {
   const int dv = p.dv;
-  if (dv <= 32) return launch_bf16<KS, 1, 2>(p, vec, stream);
-  if (dv <= 64) return launch_bf16<KS, 2, 2>(p, vec, stream);
-  return launch_bf16<KS, 4, 1>(p, vec, stream);
+  if (dv <= 32) return launch_bf16<KS, 1, 2>(p, vec, packed, stream);
+  if (dv <= 64) return launch_bf16<KS, 2, 2>(p, vec, packed, stream);
+  return launch_bf16<KS, 4, 1>(p, vec, packed, stream);
 }
 
 }  // namespace
+
+// [V^T blocks: BH * nb64 * vt_block_bytes][column-sum prefixes: BH * nb64 * DV fp32]
+size_t parallel_workspace_bytes(int BH, int N, int d, int dv, bool in_f32) {
+  if (in_f32 || !packed_shape(d, dv)) return 0;
+  const size_t nb64 = ((size_t)N + BN - 1) / BN;
+  const size_t DV = dv <= 32 ? 32 : 64;
+  return (size_t)BH * nb64 * (vt_block_bytes(dv) + DV * 4);
+}
 
 int launch_based_parallel_fp32(const ParallelArgs& a, hipStream_t stream);
 
@@ -508,6 +659,11 @@ int launch_based_parallel(const ParallelArgs& a, hipStream_t stream) {
   p.q = static_cast<const uint16_t*>(a.q);
   p.k = static_cast<const uint16_t*>(a.k);
   p.v = static_cast<const uint16_t*>(a.v);
+  p.vt = static_cast<const uint16_t*>(a.workspace);
+  p.nb64 = (a.N + BN - 1) / BN;
+  if (a.workspace != nullptr)
+    p.vpre = reinterpret_cast<const float*>(static_cast<const char*>(a.workspace) +
+                                            (size_t)a.BH * p.nb64 * vt_block_bytes(a.dv));
   p.out = a.out;
   p.den = a.den;
   p.BH = a.BH;
@@ -536,10 +692,15 @@ int launch_based_parallel(const ParallelArgs& a, hipStream_t stream) {
   const bool vec = (a.d % 8 == 0) && (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.k) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 7) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0);
-  if (a.d <= 16) return dispatch_mt<1>(p, vec, stream);
-  if (a.d <= 32) return dispatch_mt<2>(p, vec, stream);
-  if (a.d <= 64) return dispatch_mt<4>(p, vec, stream);
-  return dispatch_mt<8>(p, vec, stream);
+  // packed path: workspace present, 16-byte aligned K and workspace, 32-bit buffer offsets
+  const bool packed = vec && packed_shape(a.d, a.dv) && a.workspace != nullptr &&
+                      a.workspace_bytes >= parallel_workspace_bytes(a.BH, a.N, a.d, a.dv, false) &&
+                      ((reinterpret_cast<uintptr_t>(a.workspace) & 15) == 0) &&
+                      (size_t)p.nb64 * vt_block_bytes(a.dv) < ((size_t)1 << 30) && (size_t)a.N * 32 < ((size_t)1 << 30);
+  if (a.d <= 16) return dispatch_mt<1>(p, vec, packed, stream);
+  if (a.d <= 32) return dispatch_mt<2>(p, vec, false, stream);
+  if (a.d <= 64) return dispatch_mt<4>(p, vec, false, stream);
+  return dispatch_mt<8>(p, vec, false, stream);
 }
 
 }  // namespace la

@@ -53,21 +53,31 @@ const char* la_status_string(int status) {
   return "unknown status";
 }
 
+size_t la_based_parallel_workspace_bytes(int B, int H, int N, int d, int dv, int in_dtype) {
+  if (B < 1 || H < 1 || N < 1 || d < 1 || dv < 1) return 0;
+  return la::parallel_workspace_bytes(B * H, N, d, dv, in_dtype == LA_F32);
+}
+
 int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype,
                           float* den_or_null, int B, int H, int N, int d, int dv, float scale, float eps,
-                          int normalize, void* hip_stream) {
+                          int normalize, void* workspace, size_t workspace_bytes, void* hip_stream) {
   int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
   if (rc != LA_OK) return rc;
   if (d > 128 || dv > 128) return LA_ERR_UNSUPPORTED_DIM;
   if (!finite_f(scale) || !(scale > 0.f) || !finite_f(eps) || eps < 0.f) return LA_ERR_BAD_SCALAR;
   if ((long long)B * H * N == 0) return LA_OK;
   if (den_or_null != nullptr && (reinterpret_cast<uintptr_t>(den_or_null) & 3)) return LA_ERR_BAD_ALIGNMENT;
+  const size_t need = la::parallel_workspace_bytes(B * H, N, d, dv, in_dtype == LA_F32);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
+  if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15)) return LA_ERR_BAD_ALIGNMENT;
   la::ParallelArgs a{};
   a.q = q;
   a.k = k;
   a.v = v;
   a.out = out;
   a.den = den_or_null;
+  a.workspace = need > 0 ? workspace : nullptr;
+  a.workspace_bytes = need > 0 ? workspace_bytes : 0;
   a.BH = B * H;
   a.N = N;
   a.d = d;

@@ -52,6 +52,22 @@ __device__ __forceinline__ f32x16 mfma32x32x16_f16(u32x4 a, u32x4 b, f32x16 c) {
                                                 0, 0, 0);
 }
 
+// v_mfma_f32_16x16x32_bf16.  A (16 x 32): lane l holds row l%16, k = 8*(l/16) .. +7; B likewise
+// with col l%16; C (16 x 16): lane l holds col l%16, rows 4*(l/16) + i for i = 0..3.
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+// Packed fp16 a*b + c, one rounding per half (v_pk_fma_f16).
+__device__ __forceinline__ u32 pk_fma_f16(u32 a, u32 b, u32 c) {
+  return __builtin_bit_cast(u32, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b),
+                                                           __builtin_bit_cast(f16x2, c)));
+}
+__device__ __forceinline__ u32 pk_mul_f16(u32 a, u32 b) {
+  return __builtin_bit_cast(u32, __builtin_bit_cast(f16x2, a) * __builtin_bit_cast(f16x2, b));
+}
+
 // float -> bf16 bits, round to nearest even (the hardware conversion on gfx950).
 __device__ __forceinline__ u32 pack_bf16x2(float lo, float hi) {
   bf16x2 p = __builtin_convertvector((f32x2){lo, hi}, bf16x2);

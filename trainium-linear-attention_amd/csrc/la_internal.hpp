@@ -14,6 +14,8 @@ struct ParallelArgs {
   const void* v;
   void* out;
   float* den;          // optional, (BH, N) fp32, den without eps
+  void* workspace;     // optional scratch of parallel_workspace_bytes(); enables the packed path
+  size_t workspace_bytes;
   int BH, N, d, dv;
   float scale, eps;
   bool normalize;
@@ -55,21 +57,23 @@ struct FeatureMapArgs {
 // Each launcher validates what only it knows (supported tile shapes), launches on `stream`
 // and returns 0, a negative LA_ERR_* code, or a positive hipError_t.
 int launch_based_parallel(const ParallelArgs& a, hipStream_t stream);
+size_t parallel_workspace_bytes(int BH, int N, int d, int dv, bool in_f32);
 int launch_sliding_window(const SlidingArgs& a, hipStream_t stream);
 size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk);
 int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream);
 int launch_feature_map(const FeatureMapArgs& a, hipStream_t stream);
 
-// Work-group order for causal query blocks: heaviest (last) blocks first, and -- when the
-// head count is a multiple of the 8 XCDs -- every XCD works through whole heads in turn so a
-// head's K/V prefix stays in that XCD's L2.  Work-groups are dispatched to XCDs round-robin
-// by work-group id.
+// Work-group order for causal query blocks: heaviest (last) blocks first over all the heads an
+// XCD owns, so that greedy dispatch as slots free up balances the causal triangle (a head-major
+// order leaves the last heads' long blocks for the end).  When the head count is a multiple of
+// the 8 XCDs each XCD owns whole heads, so a head's K/V prefix is only read through one L2.
+// Work-groups are dispatched to XCDs round-robin by work-group id.
 __device__ __forceinline__ void map_causal_block(int wg, int BH, int nqb, int& bh, int& qb) {
   if ((BH & 7) == 0) {
-    const int x = wg & 7, slot = wg >> 3;
-    const int hx = slot / nqb;
-    qb = nqb - 1 - (slot - hx * nqb);
-    bh = hx * 8 + x;
+    const int x = wg & 7, slot = wg >> 3, hpx = BH >> 3;
+    const int r = slot / hpx;
+    qb = nqb - 1 - r;
+    bh = (slot - r * hpx) * 8 + x;
   } else {
     const int r = wg / BH;
     qb = nqb - 1 - r;

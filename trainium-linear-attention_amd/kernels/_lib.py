@@ -30,9 +30,10 @@ _c_size = ctypes.c_size_t
 _SIGNATURES = {
     "la_abi_version": (_c_int, []),
     "la_status_string": (ctypes.c_char_p, [_c_int]),
+    "la_based_parallel_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "la_based_parallel_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_void,
                                        _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int,
-                                       _c_void]),
+                                       _c_void, _c_size, _c_void]),
     "la_based_chunked_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "la_based_chunked_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
                                       _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int, _c_void,
@@ -42,7 +43,7 @@ _SIGNATURES = {
     "la_taylor_feature_map": (_c_int, [_c_void, _c_int, _c_void, _c_int, ctypes.c_longlong, _c_int, _c_void]),
 }
 
-EXPECTED_ABI = 1
+EXPECTED_ABI = 2
 
 
 class BasedLAError(RuntimeError):

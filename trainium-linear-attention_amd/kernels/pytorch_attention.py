@@ -75,9 +75,13 @@ def based_parallel(q, k, v, eps=1e-6, scale=None, normalize=True, out_dtype=None
     qc, kc, vc = (_as_kernel_input(x, cdt) for x in (q, k, v))
     out = torch.empty(b, h, t, dv, dtype=kdt, device=q.device)
     den = torch.empty(b, h, t, dtype=torch.float32, device=q.device) if return_den else None
-    rc = _lib.lib().la_based_parallel_fwd(
+    L = _lib.lib()
+    ws_bytes = int(L.la_based_parallel_workspace_bytes(b, h, t, d, dv, _lib.dtype_code(cdt)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    rc = L.la_based_parallel_fwd(
         _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.dtype_code(cdt), _lib.ptr(out), _lib.dtype_code(kdt),
-        _lib.ptr(den), b, h, t, d, dv, float(scale), float(eps), 1 if normalize else 0, _lib.stream_of(q))
+        _lib.ptr(den), b, h, t, d, dv, float(scale), float(eps), 1 if normalize else 0, _lib.ptr(ws), ws_bytes,
+        _lib.stream_of(q))
     _lib.check(rc, "la_based_parallel_fwd")
     if out.dtype != odt:
         out = out.to(odt)
