@@ -180,14 +180,19 @@ __global__ __launch_bounds__(256) void colsum_scan_kernel(float* __restrict__ co
 
 // UNIT: 1/c scales to exactly 1 (scale = 1/sqrt(d) with d a power of 4), so the score MFMA
 // starts from the inline constant 1.0 and u = b*b - 1.
-template <int KS, int MT, int QT, bool VEC, bool UNIT, bool PACKED>
-__global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const ParallelParams p) {
-  constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128 * QT, NSNAP = BM / BN;
+//
+// NW waves per work-group (4, or 8 on the packed path, where the registers are capped so that
+// four waves share each SIMD).
+template <int KS, int MT, int QT, bool VEC, bool UNIT, bool PACKED, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 4 : 1)))
+void based_parallel_bf16_kernel(const ParallelParams p) {
+  constexpr int DK = 16 * KS, DV = 32 * MT, BM = 32 * QT * NW, NSNAP = BM / BN;
   constexpr int KROW = DK + 8;
   constexpr int LPR = 256 / DV;      // threads per V^T row in the running column sum
   constexpr int KPL = BN / LPR;      // keys per thread in the running column sum
   using Stager = BlockStager<KS, MT, VEC, true>;
   static_assert(!PACKED || KS == 1, "the packed path is for d = 16");
+  static_assert(NW == 4 || (PACKED && NW == 8), "register staging assumes 4 waves");
   constexpr int NVU = VtBlock<DV>::units;
   constexpr int NU = 2 + NVU;                       // 1 KB copy units per block: K (2), V^T
   constexpr int STAGE = 1024 + NVU * 512;           // halves per packed stage: K, then V^T
@@ -256,17 +261,18 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
 
   const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
 
-  // ---- packed path: global -> LDS copies.  Wave wu owns units wu, wu + 4, wu + 8 of every
+  // ---- packed path: global -> LDS copies.  Wave wu owns units wu, wu + NW, ... of every
   // block; unit u lands at byte 1024 u of the stage (K units 0-1, V^T units 2..).
+  constexpr int UPW = (NU + NW - 1) / NW;   // most units per wave
   const int wu = __builtin_amdgcn_readfirstlane(w);
-  const int my_units = NU / 4 + (wu < NU % 4 ? 1 : 0);
+  const int my_units = NU / NW + (wu < NU % NW ? 1 : 0);
   constexpr int VTB = VtBlock<DV>::bytes;
   const u32x4 rk = buffer_rsrc(kg, (u32)N * 32u);
   const u32x4 rv = buffer_rsrc(p.vt + (size_t)bh * p.nb64 * (VTB / 2), (u32)p.nb64 * (u32)VTB);
-  int uoff[3];
+  int uoff[UPW];
 #pragma unroll
-  for (int i = 0; i < 3; ++i) {
-    const int u = wu + 4 * i;
+  for (int i = 0; i < UPW; ++i) {
+    const int u = wu + NW * i;
     if (u < 2) {
       // K slot sl = 2 key + (c ^ ((key >> 2) & 1)) holds 16-byte chunk c of the key's row
       const int sl = 64 * u + lane, key = sl >> 1, c = (sl & 1) ^ ((key >> 2) & 1);
@@ -278,8 +284,8 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
   auto issue = [&](int blk) {
     const u32 base = lds_addr(&stage[blk % NRAW][0]);
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
-      const int u = wu + 4 * i;
+    for (int i = 0; i < UPW; ++i) {
+      const int u = wu + NW * i;
       if (u >= NU) break;
       if (u < 2)
         lds_copy16(rk, base + 1024 * u, uoff[i] + blk * (BN * 32));
@@ -603,33 +609,42 @@ __global__ __launch_bounds__(256) void based_parallel_bf16_kernel(const Parallel
   }
 }
 
+// Packed path: pre-pass, column-sum scan, then the main kernel with 4 waves x 64 queries (8 waves
+// x 32 queries at four waves per SIMD measured slower).
+template <int MT>
+int launch_packed(const ParallelParams& pp, hipStream_t stream) {
+  constexpr int DV = 32 * MT, QT = 2, NW = 4, BM = 32 * QT * NW;
+  ParallelParams p = pp;
+  p.nqb = (p.N + BM - 1) / BM;
+  const dim3 grid((unsigned)(p.nqb * p.BH)), block(64 * NW);
+  const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
+  hipLaunchKernelGGL((vt_pack_kernel<DV>), dim3((unsigned)p.nb64, (unsigned)p.BH), dim3(256), 0, stream, p.v,
+                     const_cast<uint16_t*>(p.vt), const_cast<float*>(p.vpre), p.N, p.dv, p.nb64);
+  hipLaunchKernelGGL((colsum_scan_kernel<DV>), dim3((unsigned)p.BH), dim3(256), 0, stream,
+                     const_cast<float*>(p.vpre), p.nb64);
+  if (unit)
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<1, MT, QT, true, true, true, NW>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<1, MT, QT, true, false, true, NW>), grid, block, 0, stream, p);
+  return (int)hipGetLastError();
+}
+
 template <int KS, int MT, int QT>
 int launch_bf16(const ParallelParams& pp, bool vec, bool packed, hipStream_t stream) {
+  if constexpr (KS == 1 && MT <= 2) {
+    if (packed) return launch_packed<MT>(pp, stream);
+  }
   constexpr int BM = 128 * QT;
   ParallelParams p = pp;
   p.nqb = (p.N + BM - 1) / BM;
   const dim3 grid((unsigned)(p.nqb * p.BH)), block(256);
   const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
-  if constexpr (KS == 1 && MT <= 2) {
-    if (packed) {
-      constexpr int DV = 32 * MT;
-      hipLaunchKernelGGL((vt_pack_kernel<DV>), dim3((unsigned)p.nb64, (unsigned)p.BH), dim3(256), 0, stream, p.v,
-                         const_cast<uint16_t*>(p.vt), const_cast<float*>(p.vpre), p.N, p.dv, p.nb64);
-      hipLaunchKernelGGL((colsum_scan_kernel<DV>), dim3((unsigned)p.BH), dim3(256), 0, stream,
-                         const_cast<float*>(p.vpre), p.nb64);
-      if (unit)
-        hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, true, true>), grid, block, 0, stream, p);
-      else
-        hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, false, true>), grid, block, 0, stream, p);
-      return (int)hipGetLastError();
-    }
-  }
   if (vec && unit)
-    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, true, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, true, false, 4>), grid, block, 0, stream, p);
   else if (vec)
-    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, false, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, false, false, 4>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, false, false, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, false, false, false, 4>), grid, block, 0, stream, p);
   return (int)hipGetLastError();
 }
 
