@@ -73,7 +73,7 @@ struct ChunkParams {
   float W;                            // weight of "1" in intra u units; q-side phi carries it too
   float st_lin, st_diag, st_off;      // internal -> reference feature basis factors (state export)
   u32 ones_hi, ones_lo;
-  int normalize, out_f32, vec;
+  int normalize, out_f32, vec, vec_out;   // vec_out: dv % 4 == 0 and out 16-byte aligned
 };
 
 __device__ __forceinline__ void map_segment(int wg, int BH, int P, int& bh, int& p) {
@@ -342,35 +342,45 @@ __global__ __launch_bounds__(256, 2) void chunked_segment_kernel(const ChunkPara
 }
 
 // -------------------------------------------------------------------------------------------
-// Kernel 1b: exclusive prefix over segments, in place.  Thread (head, element); after it, slot
-// p - 1 holds sum_{p' < p} of the increments (S as fp16, z and sum v as fp32).
+// Kernel 1b: inclusive prefix over segments, in place.  Thread (head, element); after it, slot
+// p - 1 holds sum_{p' < p} of the increments (S as fp16, z and sum v as fp32).  Values are read
+// 16 segments at a time with all loads in flight before the first store.
+template <class T>
+__device__ __forceinline__ float to_f(T x) {
+  if constexpr (sizeof(T) == 2) return (float)__builtin_bit_cast(_Float16, x);
+  else return x;
+}
+template <class T>
+__device__ __forceinline__ T from_f(float x) {
+  if constexpr (sizeof(T) == 2) return __builtin_bit_cast(uint16_t, (_Float16)x);
+  else return x;
+}
+template <class T>
+__device__ __forceinline__ void prefix_scan(T* base, size_t stride, int nseg) {
+  float acc = 0.f;
+  for (int s0 = 0; s0 < nseg; s0 += 16) {
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = s0 + i < nseg ? to_f(base[(size_t)(s0 + i) * stride]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc += x[i];
+      if (s0 + i < nseg) base[(size_t)(s0 + i) * stride] = from_f<T>(acc);
+    }
+  }
+}
 __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p) {
   constexpr int NS_ELEM = DVC * NF, NE = NS_ELEM + NF + DVC;
   const int e = blockIdx.x * 256 + threadIdx.x;
   const int bh = blockIdx.y;
   if (e >= NE) return;
   const int nseg = p.P - 1;
-  float acc = 0.f;
-  if (e < NS_ELEM) {
-    uint16_t* base = p.wsS + (size_t)bh * p.P * NS_ELEM + e;
-    for (int sp = 0; sp < nseg; ++sp) {
-      uint16_t* ptr = base + (size_t)sp * NS_ELEM;
-      acc += (float)__builtin_bit_cast(_Float16, *ptr);
-      *ptr = __builtin_bit_cast(uint16_t, (_Float16)acc);
-    }
-  } else if (e < NS_ELEM + NF) {
-    float* base = p.wsZ + (size_t)bh * p.P * NF + (e - NS_ELEM);
-    for (int sp = 0; sp < nseg; ++sp) {
-      acc += base[(size_t)sp * NF];
-      base[(size_t)sp * NF] = acc;
-    }
-  } else {
-    float* base = p.wsV + (size_t)bh * p.P * DVC + (e - NS_ELEM - NF);
-    for (int sp = 0; sp < nseg; ++sp) {
-      acc += base[(size_t)sp * DVC];
-      base[(size_t)sp * DVC] = acc;
-    }
-  }
+  if (e < NS_ELEM)
+    prefix_scan(p.wsS + (size_t)bh * p.P * NS_ELEM + e, NS_ELEM, nseg);
+  else if (e < NS_ELEM + NF)
+    prefix_scan(p.wsZ + (size_t)bh * p.P * NF + (e - NS_ELEM), NF, nseg);
+  else
+    prefix_scan(p.wsV + (size_t)bh * p.P * DVC + (e - NS_ELEM - NF), DVC, nseg);
 }
 
 // -------------------------------------------------------------------------------------------
@@ -510,7 +520,7 @@ __global__ __launch_bounds__(256, 2) void chunked_output_kernel(const ChunkParam
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt) {
         const u32x4 b = *reinterpret_cast<const u32x4*>(&L.ST[(16 * nt + r) * STS + 32 * ks + 8 * g]);
-        O[nt] = mfma16_f16(a, b, O[nt]);
+        O[nt] = mfma16_f16(b, a, O[nt]);
       }
     }
 
@@ -565,15 +575,15 @@ __global__ __launch_bounds__(256, 2) void chunked_output_kernel(const ChunkParam
         const u32x2 a0 = *reinterpret_cast<const u32x2*>(vp);
         const u32x2 a1 = *reinterpret_cast<const u32x2*>(vp + 16);
         const u32x4 vb = {a0[0], a0[1], a1[0], a1[1]};
-        O[nt] = mfma16_f16(pa, vb, O[nt]);
-        O[nt] = mfma16_f16(mk, vb, O[nt]);
+        O[nt] = mfma16_f16(vb, pa, O[nt]);
+        O[nt] = mfma16_f16(vb, mk, O[nt]);
         if (p.ones_lo != 0u) {
           u32x4 ml;
 #pragma unroll
           for (int t = 0; t < 4; ++t)
             ml[t] = ((mk[t] & 0xffffu) ? (p.ones_lo & 0xffffu) : 0u) |
                     ((mk[t] & 0xffff0000u) ? (p.ones_lo & 0xffff0000u) : 0u);
-          O[nt] = mfma16_f16(ml, vb, O[nt]);
+          O[nt] = mfma16_f16(vb, ml, O[nt]);
         }
       }
     }
@@ -591,24 +601,38 @@ __global__ __launch_bounds__(256, 2) void chunked_output_kernel(const ChunkParam
     else
       update_slots<2>(L, S, z, w, lane);
 
-    // ---- outputs: C layout, lane (dv col 16nt + r, tokens 4g + i of this wave)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * w + 4 * g + i;
-      const int row = row0 + t;
-      const float den = __shfl(den_a, 4 * g + i);
-      const float inv = p.normalize ? 1.0f / (den + p.eps) : 1.0f;
+    // ---- outputs.  O is kept transposed (the 16x16 MFMAs above take V^T / S^T as A), so lane
+    // (token tl, dv rows 16nt + 4g .. +3) holds four consecutive outputs of its own token.
+    {
+      const int row = row0 + tl;
+      const float inv = p.normalize ? 1.0f / (den_a + p.eps) : 1.0f;
       if (row < N) {
+        const size_t obase = (size_t)(hrow + row) * dv;
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
-          const int col = 16 * nt + r;
-          if (col < dv) {
-            const float y = (L.S0[col] + O[nt][i] * p.fscale) * inv;
-            const size_t o = (size_t)(hrow + row) * dv + col;
-            if (p.out_f32)
-              static_cast<float*>(p.out)[o] = y;
-            else
-              static_cast<uint16_t*>(p.out)[o] = f32_to_bf16_bits(y);
+          const int col = 16 * nt + 4 * g;
+          const f4 s0 = *reinterpret_cast<const f4*>(&L.S0[col]);
+          float y[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) y[i] = (s0[i] + O[nt][i] * p.fscale) * inv;
+          if (p.vec_out) {
+            if (col < dv) {
+              if (p.out_f32)
+                *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + obase + col) = (f32x4){y[0], y[1], y[2], y[3]};
+              else
+                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + obase + col) =
+                    (u32x2){pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if (col + i < dv) {
+                if (p.out_f32)
+                  static_cast<float*>(p.out)[obase + col + i] = y[i];
+                else
+                  static_cast<uint16_t*>(p.out)[obase + col + i] = f32_to_bf16_bits(y[i]);
+              }
+            }
           }
         }
       }
@@ -733,6 +757,7 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
   const bool vec = (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.k) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 7) == 0);
   p.vec = vec;
+  p.vec_out = (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0);
   const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
   if (P > 1) {
     const dim3 grid((unsigned)(a.BH * (P - 1)));

@@ -40,6 +40,7 @@
 // Other shapes stage K and V through registers into a double-buffered LDS block.
 #include "la_common.hpp"
 #include "la_internal.hpp"
+#include "la_pack.hpp"
 #include "la_stage.hpp"
 
 namespace la {
@@ -63,66 +64,12 @@ struct ParallelParams {
 
 constexpr int NRAW = 7;   // LDS stages of the packed path
 
-// Packed V^T block: DV rows of VROW fp16 (keys 0..63 + padding), rounded up to whole 1 KB
-// copy units.
 template <int DV>
-struct VtBlock {
-  static constexpr int units = (DV * VROW * 2 + 1023) / 1024;
-  static constexpr int bytes = units * 1024;
-};
+using VtBlockP = VtBlock<DV, VROW>;
 
-size_t vt_block_bytes(int dv) { return dv <= 32 ? (size_t)VtBlock<32>::bytes : (size_t)VtBlock<64>::bytes; }
+size_t vt_block_bytes(int dv) { return dv <= 32 ? (size_t)VtBlockP<32>::bytes : (size_t)VtBlockP<64>::bytes; }
 
 bool packed_shape(int d, int dv) { return d == 16 && dv % 8 == 0 && dv <= 64; }
-
-// V (bf16 [N][dv]) of one head -> fp16 V^T blocks [nb64][DV][VROW], zero for keys >= N,
-// rows >= dv and the padding.
-// Also writes the column sums of the block, colsum[bh][blk][DV].
-template <int DV>
-__global__ __launch_bounds__(256) void vt_pack_kernel(const uint16_t* __restrict__ v, uint16_t* __restrict__ vt,
-                                                      float* __restrict__ colsum, int N, int dv, int nb64) {
-  constexpr int NP = 256 / DV;   // partial sums per column
-  __shared__ float tile[BN][DV + 1];
-  __shared__ float part[NP][DV];
-  const int blk = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
-  const int row0 = blk * BN;
-  const uint16_t* __restrict__ src = v + ((size_t)bh * N + row0) * dv;
-  constexpr int NLD = BN * (DV / 2) / 256;   // bf16 pairs per thread
-  u32 x[NLD];
-#pragma unroll
-  for (int i = 0; i < NLD; ++i) {   // all loads in flight before the first LDS store
-    const int idx = tid + 256 * i, key = idx / (DV / 2), col = 2 * (idx % (DV / 2));
-    x[i] = (row0 + key < N && col < dv) ? *reinterpret_cast<const u32*>(src + (size_t)key * dv + col) : 0u;
-  }
-#pragma unroll
-  for (int i = 0; i < NLD; ++i) {
-    const int idx = tid + 256 * i, key = idx / (DV / 2), col = 2 * (idx % (DV / 2));
-    tile[key][col] = bf16_lo_to_f32(x[i]);
-    tile[key][col + 1] = bf16_hi_to_f32(x[i]);
-  }
-  __syncthreads();
-  u32* __restrict__ dst = reinterpret_cast<u32*>(vt + ((size_t)bh * nb64 + blk) * (VtBlock<DV>::bytes / 2));
-  for (int idx = tid; idx < VtBlock<DV>::bytes / 4; idx += 256) {
-    const int row = (2 * idx) / VROW, col = (2 * idx) % VROW;
-    u32 y = 0u;
-    if (row < DV && col < BN) y = pack_f16x2(tile[col][row], tile[col + 1][row]);
-    dst[idx] = y;
-  }
-  {
-    const int col = tid % DV, pi = tid / DV;
-    float t = 0.f;
-#pragma unroll
-    for (int key = pi * (BN / NP); key < (pi + 1) * (BN / NP); ++key) t += tile[key][col];
-    part[pi][col] = t;
-  }
-  __syncthreads();
-  if (tid < DV) {
-    float t = 0.f;
-#pragma unroll
-    for (int pi = 0; pi < NP; ++pi) t += part[pi][tid];
-    colsum[((size_t)bh * nb64 + blk) * DV + tid] = t;
-  }
-}
 
 // colsum[bh][blk][DV] -> exclusive prefix over blk, in place.  One work-group per head; the
 // head's column sums go through LDS in tiles of 4096 values (all loads of a tile in flight at
@@ -193,7 +140,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   using Stager = BlockStager<KS, MT, VEC, true>;
   static_assert(!PACKED || KS == 1, "the packed path is for d = 16");
   static_assert(NW == 4 || (PACKED && NW == 8), "register staging assumes 4 waves");
-  constexpr int NVU = VtBlock<DV>::units;
+  constexpr int NVU = VtBlockP<DV>::units;
   constexpr int NU = 2 + NVU;                       // 1 KB copy units per block: K (2), V^T
   constexpr int STAGE = 1024 + NVU * 512;           // halves per packed stage: K, then V^T
 
@@ -266,7 +213,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   constexpr int UPW = (NU + NW - 1) / NW;   // most units per wave
   const int wu = __builtin_amdgcn_readfirstlane(w);
   const int my_units = NU / NW + (wu < NU % NW ? 1 : 0);
-  constexpr int VTB = VtBlock<DV>::bytes;
+  constexpr int VTB = VtBlockP<DV>::bytes;
   const u32x4 rk = buffer_rsrc(kg, (u32)N * 32u);
   const u32x4 rv = buffer_rsrc(p.vt + (size_t)bh * p.nb64 * (VTB / 2), (u32)p.nb64 * (u32)VTB);
   int uoff[UPW];
@@ -618,7 +565,7 @@ int launch_packed(const ParallelParams& pp, hipStream_t stream) {
   p.nqb = (p.N + BM - 1) / BM;
   const dim3 grid((unsigned)(p.nqb * p.BH)), block(64 * NW);
   const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
-  hipLaunchKernelGGL((vt_pack_kernel<DV>), dim3((unsigned)p.nb64, (unsigned)p.BH), dim3(256), 0, stream, p.v,
+  hipLaunchKernelGGL((vt_pack_kernel<DV, VROW, true, true>), dim3((unsigned)p.nb64, (unsigned)p.BH), dim3(256), 0, stream, p.v,
                      const_cast<uint16_t*>(p.vt), const_cast<float*>(p.vpre), p.N, p.dv, p.nb64);
   hipLaunchKernelGGL((colsum_scan_kernel<DV>), dim3((unsigned)p.BH), dim3(256), 0, stream,
                      const_cast<float*>(p.vpre), p.nb64);

@@ -51,9 +51,13 @@ def _check_qkv(q, k, v):
 
 
 def _as_kernel_input(x: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
+    """x in dtype dt, contiguous and 16-byte aligned (the kernels copy rows 16 bytes at a time)."""
     if x.dtype != dt:
         x = x.to(dt)
-    return x.contiguous()
+    x = x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    return x
 
 
 def based_parallel(q, k, v, eps=1e-6, scale=None, normalize=True, out_dtype=None, return_den=False):
