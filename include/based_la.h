@@ -70,6 +70,24 @@ int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dt
                           void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /*
+ * The two halves of la_based_parallel_fwd for shapes that use the workspace: the V pre-pass,
+ * and the attention kernel reading a workspace that already holds the pre-pass of the same v
+ * (several calls with one v, or timing the attention kernel alone).  No counterpart in the
+ * reference, whose parallel kernel has no pre-pass (kernels/nki_attention.py:33-115).  For
+ * shapes with la_based_parallel_workspace_bytes(...) == 0 the pack is a no-op and
+ * la_based_parallel_fwd_packed is la_based_parallel_fwd.  The packed kernels need q, k, out
+ * 16-byte and v 8-byte aligned (LA_ERR_BAD_ALIGNMENT otherwise; la_based_parallel_fwd instead
+ * falls back to its unpacked kernel).
+ */
+int la_based_parallel_pack(const void* v, int in_dtype, int B, int H, int N, int d, int dv,
+                           void* workspace, size_t workspace_bytes, void* hip_stream);
+int la_based_parallel_fwd_packed(const void* q, const void* k, const void* v, int in_dtype,
+                                 void* out, int out_dtype, float* den_or_null,
+                                 int B, int H, int N, int d, int dv,
+                                 float scale, float eps, int normalize,
+                                 void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/*
  * Chunked recurrent BASED attention (linear in N).
  *
  * Replaces chunked_nki_numerator / the NKI chunked kernel:

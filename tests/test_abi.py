@@ -26,7 +26,7 @@ def _lib():
 def test_header_declares_expected_entry_points():
     assert _declared() == sorted([
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
-        "la_based_chunked_workspace_bytes", "la_based_chunked_fwd", "la_sliding_window_fwd",
+        "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_fwd", "la_sliding_window_fwd",
         "la_taylor_feature_map"])
 
 
@@ -80,6 +80,24 @@ def test_parallel_argument_errors():
     assert call(ws=ctypes.c_void_p(24)) == -8
     assert call(N=0) == 0          # empty: nothing to launch
     assert call(B=0) == 0
+
+
+def test_parallel_pack_and_packed_argument_errors():
+    lib = _lib()
+    need = lib.la_based_parallel_workspace_bytes(1, 1, 8, 16, 64, 1)
+    pack = lib.la_based_parallel_pack
+    assert pack(None, 1, 1, 1, 8, 16, 64, P, need, None) == -1
+    assert pack(P, 1, 1, 1, 8, 16, 64, None, need, None) == -6
+    assert pack(ctypes.c_void_p(24), 1, 1, 1, 8, 16, 64, P, need, None) == -8   # v not 16-byte aligned
+    assert pack(P, 0, 1, 1, 8, 16, 64, None, 0, None) == 0                       # fp32: nothing to pack
+    f = lib.la_based_parallel_fwd_packed
+    a = [P, P, P, 1, P, 1, None, 1, 1, 8, 16, 64, 0.25, 1e-6, 1, P, need, None]
+    a_bad = list(a)
+    a_bad[4] = ctypes.c_void_p(40)                                               # out 8- but not 16-byte aligned
+    assert f(*a_bad) == -8
+    a_bad = list(a)
+    a_bad[15] = None
+    assert f(*a_bad) == -6
 
 
 def test_parallel_workspace_sizes():

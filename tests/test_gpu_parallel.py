@@ -170,3 +170,35 @@ def test_single_hip_runtime_and_native_library():
     rts = _lib.hip_runtimes_loaded()
     print("HIP runtimes mapped:", rts)
     assert len(rts) == 1
+
+
+@pytest.mark.parametrize("B,H,N,dv", [(1, 2, 777, 64), (2, 8, 1024, 32)])
+def test_pack_then_packed_kernel_equals_fused_call(B, H, N, dv):
+    """la_based_parallel_pack + la_based_parallel_fwd_packed is la_based_parallel_fwd, bit for
+    bit, including a second v packed into the same workspace."""
+    from kernels import _lib
+    L = _lib.lib()
+    d = 16
+    ws_bytes = int(L.la_based_parallel_workspace_bytes(B, H, N, d, dv, 1))
+    assert ws_bytes > 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    for seed in (11, 12):
+        q, k, v = to_dev(*rand_qkv(B, H, N, d, dv, seed=seed, dtype=torch.bfloat16, scale_qk=0.5))
+        outs = []
+        for mode in ("fused", "split"):
+            out = torch.empty(B, H, N, dv, dtype=torch.float32, device="cuda")
+            den = torch.empty(B, H, N, dtype=torch.float32, device="cuda")
+            args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), 1, out.data_ptr(), 0, den.data_ptr(), B, H, N, d, dv,
+                    0.25, 1e-6, 1, ws.data_ptr(), ws_bytes, st)
+            if mode == "fused":
+                assert L.la_based_parallel_fwd(*args) == 0
+            else:
+                assert L.la_based_parallel_pack(v.data_ptr(), 1, B, H, N, d, dv, ws.data_ptr(), ws_bytes, st) == 0
+                assert L.la_based_parallel_fwd_packed(*args) == 0
+            outs.append((out, den))
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+        want, _, want_den = ref.based_dense(q.cpu(), k.cpu(), v.cpu())
+        assert err(outs[1][0], want) < TOL_BF16
+        assert err(outs[1][1], want_den) < TOL_BF16

@@ -559,28 +559,33 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
 // Packed path: pre-pass, column-sum scan, then the main kernel with 4 waves x 64 queries (8 waves
 // x 32 queries at four waves per SIMD measured slower).
 template <int MT>
-int launch_packed(const ParallelParams& pp, hipStream_t stream) {
+int launch_packed(const ParallelParams& pp, int stages, hipStream_t stream) {
   constexpr int DV = 32 * MT, QT = 2, NW = 4, BM = 32 * QT * NW;
   ParallelParams p = pp;
   p.nqb = (p.N + BM - 1) / BM;
-  const dim3 grid((unsigned)(p.nqb * p.BH)), block(64 * NW);
-  const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
-  hipLaunchKernelGGL((vt_pack_kernel<DV, VROW, true, true>), dim3((unsigned)p.nb64, (unsigned)p.BH), dim3(256), 0, stream, p.v,
-                     const_cast<uint16_t*>(p.vt), const_cast<float*>(p.vpre), p.N, p.dv, p.nb64);
-  hipLaunchKernelGGL((colsum_scan_kernel<DV>), dim3((unsigned)p.BH), dim3(256), 0, stream,
-                     const_cast<float*>(p.vpre), p.nb64);
-  if (unit)
-    hipLaunchKernelGGL((based_parallel_bf16_kernel<1, MT, QT, true, true, true, NW>), grid, block, 0, stream, p);
-  else
-    hipLaunchKernelGGL((based_parallel_bf16_kernel<1, MT, QT, true, false, true, NW>), grid, block, 0, stream, p);
+  if (stages & 1) {
+    hipLaunchKernelGGL((vt_pack_kernel<DV, VROW, true, true>), dim3((unsigned)p.nb64, (unsigned)p.BH), dim3(256), 0,
+                       stream, p.v, const_cast<uint16_t*>(p.vt), const_cast<float*>(p.vpre), p.N, p.dv, p.nb64);
+    hipLaunchKernelGGL((colsum_scan_kernel<DV>), dim3((unsigned)p.BH), dim3(256), 0, stream,
+                       const_cast<float*>(p.vpre), p.nb64);
+  }
+  if (stages & 2) {
+    const dim3 grid((unsigned)(p.nqb * p.BH)), block(64 * NW);
+    const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
+    if (unit)
+      hipLaunchKernelGGL((based_parallel_bf16_kernel<1, MT, QT, true, true, true, NW>), grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL((based_parallel_bf16_kernel<1, MT, QT, true, false, true, NW>), grid, block, 0, stream, p);
+  }
   return (int)hipGetLastError();
 }
 
 template <int KS, int MT, int QT>
-int launch_bf16(const ParallelParams& pp, bool vec, bool packed, hipStream_t stream) {
+int launch_bf16(const ParallelParams& pp, bool vec, bool packed, int stages, hipStream_t stream) {
   if constexpr (KS == 1 && MT <= 2) {
-    if (packed) return launch_packed<MT>(pp, stream);
+    if (packed) return launch_packed<MT>(pp, stages, stream);
   }
+  if (!(stages & 2)) return 0;
   constexpr int BM = 128 * QT;
   ParallelParams p = pp;
   p.nqb = (p.N + BM - 1) / BM;
@@ -596,11 +601,11 @@ int launch_bf16(const ParallelParams& pp, bool vec, bool packed, hipStream_t str
 }
 
 template <int KS>
-int dispatch_mt(const ParallelParams& p, bool vec, bool packed, hipStream_t stream) {
+int dispatch_mt(const ParallelParams& p, bool vec, bool packed, int stages, hipStream_t stream) {
   const int dv = p.dv;
-  if (dv <= 32) return launch_bf16<KS, 1, 2>(p, vec, packed, stream);
-  if (dv <= 64) return launch_bf16<KS, 2, 2>(p, vec, packed, stream);
-  return launch_bf16<KS, 4, 1>(p, vec, packed, stream);
+  if (dv <= 32) return launch_bf16<KS, 1, 2>(p, vec, packed, stages, stream);
+  if (dv <= 64) return launch_bf16<KS, 2, 2>(p, vec, packed, stages, stream);
+  return launch_bf16<KS, 4, 1>(p, vec, packed, stages, stream);
 }
 
 }  // namespace
@@ -616,7 +621,7 @@ size_t parallel_workspace_bytes(int BH, int N, int d, int dv, bool in_f32) {
 int launch_based_parallel_fp32(const ParallelArgs& a, hipStream_t stream);
 
 int launch_based_parallel(const ParallelArgs& a, hipStream_t stream) {
-  if (a.in_f32) return launch_based_parallel_fp32(a, stream);
+  if (a.in_f32) return (a.stages & 2) ? launch_based_parallel_fp32(a, stream) : 0;
   ParallelParams p{};
   p.q = static_cast<const uint16_t*>(a.q);
   p.k = static_cast<const uint16_t*>(a.k);
@@ -654,15 +659,15 @@ int launch_based_parallel(const ParallelArgs& a, hipStream_t stream) {
   const bool vec = (a.d % 8 == 0) && (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.k) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 7) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0);
-  // packed path: workspace present, 16-byte aligned K and workspace, 32-bit buffer offsets
-  const bool packed = vec && packed_shape(a.d, a.dv) && a.workspace != nullptr &&
+  // packed path: the shape takes it, the workspace is there, and the sizes fit the 32-bit
+  // buffer offsets.  The caller checked alignment (packed_alignment_ok).
+  const bool packed = packed_shape(a.d, a.dv) && a.workspace != nullptr &&
                       a.workspace_bytes >= parallel_workspace_bytes(a.BH, a.N, a.d, a.dv, false) &&
-                      ((reinterpret_cast<uintptr_t>(a.workspace) & 15) == 0) &&
                       (size_t)p.nb64 * vt_block_bytes(a.dv) < ((size_t)1 << 30) && (size_t)a.N * 32 < ((size_t)1 << 30);
-  if (a.d <= 16) return dispatch_mt<1>(p, vec, packed, stream);
-  if (a.d <= 32) return dispatch_mt<2>(p, vec, false, stream);
-  if (a.d <= 64) return dispatch_mt<4>(p, vec, false, stream);
-  return dispatch_mt<8>(p, vec, false, stream);
+  if (a.d <= 16) return dispatch_mt<1>(p, vec, packed, a.stages, stream);
+  if (a.d <= 32) return dispatch_mt<2>(p, vec, false, a.stages, stream);
+  if (a.d <= 64) return dispatch_mt<4>(p, vec, false, a.stages, stream);
+  return dispatch_mt<8>(p, vec, false, a.stages, stream);
 }
 
 }  // namespace la

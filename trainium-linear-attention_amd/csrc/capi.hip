@@ -58,26 +58,36 @@ size_t la_based_parallel_workspace_bytes(int B, int H, int N, int d, int dv, int
   return la::parallel_workspace_bytes(B * H, N, d, dv, in_dtype == LA_F32);
 }
 
-int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype,
-                          float* den_or_null, int B, int H, int N, int d, int dv, float scale, float eps,
-                          int normalize, void* workspace, size_t workspace_bytes, void* hip_stream) {
+namespace {
+
+bool al(const void* ptr, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(ptr) & (bytes - 1)) == 0; }
+
+// Shared body of the parallel entry points.  stages: 1 = pre-pass only, 2 = main kernel only
+// (workspace already holds the pre-pass of this v), 3 = both.
+int parallel_entry(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype,
+                   float* den_or_null, int B, int H, int N, int d, int dv, float scale, float eps, int normalize,
+                   void* workspace, size_t workspace_bytes, void* hip_stream, int stages) {
   int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
   if (rc != LA_OK) return rc;
   if (d > 128 || dv > 128) return LA_ERR_UNSUPPORTED_DIM;
   if (!finite_f(scale) || !(scale > 0.f) || !finite_f(eps) || eps < 0.f) return LA_ERR_BAD_SCALAR;
   if ((long long)B * H * N == 0) return LA_OK;
-  if (den_or_null != nullptr && (reinterpret_cast<uintptr_t>(den_or_null) & 3)) return LA_ERR_BAD_ALIGNMENT;
+  if (den_or_null != nullptr && !al(den_or_null, 4)) return LA_ERR_BAD_ALIGNMENT;
   const size_t need = la::parallel_workspace_bytes(B * H, N, d, dv, in_dtype == LA_F32);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
-  if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15)) return LA_ERR_BAD_ALIGNMENT;
+  if (need > 0 && !al(workspace, 16)) return LA_ERR_BAD_ALIGNMENT;
+  // the packed kernels copy q, k, v^T rows 16 bytes at a time and store out 8 bytes at a time
+  const bool aligned = al(q, 16) && al(k, 16) && al(v, 8) && al(out, 16);
+  if (need > 0 && stages != 3 && !aligned) return LA_ERR_BAD_ALIGNMENT;
   la::ParallelArgs a{};
   a.q = q;
   a.k = k;
   a.v = v;
   a.out = out;
   a.den = den_or_null;
-  a.workspace = need > 0 ? workspace : nullptr;
-  a.workspace_bytes = need > 0 ? workspace_bytes : 0;
+  a.workspace = (need > 0 && aligned) ? workspace : nullptr;
+  a.workspace_bytes = (need > 0 && aligned) ? workspace_bytes : 0;
+  a.stages = a.workspace != nullptr ? stages : (stages & 2 ? 3 : 0);
   a.BH = B * H;
   a.N = N;
   a.d = d;
@@ -87,7 +97,32 @@ int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dt
   a.normalize = normalize != 0;
   a.in_f32 = in_dtype == LA_F32;
   a.out_f32 = out_dtype == LA_F32;
+  if (a.stages == 0) return LA_OK;
   return la::launch_based_parallel(a, static_cast<hipStream_t>(hip_stream));
+}
+
+}  // namespace
+
+int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype,
+                          float* den_or_null, int B, int H, int N, int d, int dv, float scale, float eps,
+                          int normalize, void* workspace, size_t workspace_bytes, void* hip_stream) {
+  return parallel_entry(q, k, v, in_dtype, out, out_dtype, den_or_null, B, H, N, d, dv, scale, eps, normalize,
+                        workspace, workspace_bytes, hip_stream, 3);
+}
+
+int la_based_parallel_pack(const void* v, int in_dtype, int B, int H, int N, int d, int dv, void* workspace,
+                           size_t workspace_bytes, void* hip_stream) {
+  // q, k and out are not touched by the pre-pass; v stands in for them in the shared checks
+  return parallel_entry(v, v, v, in_dtype, const_cast<void*>(v), in_dtype, nullptr, B, H, N, d, dv, 1.0f, 0.f, 1,
+                        workspace, workspace_bytes, hip_stream, 1);
+}
+
+int la_based_parallel_fwd_packed(const void* q, const void* k, const void* v, int in_dtype, void* out,
+                                 int out_dtype, float* den_or_null, int B, int H, int N, int d, int dv, float scale,
+                                 float eps, int normalize, void* workspace, size_t workspace_bytes,
+                                 void* hip_stream) {
+  return parallel_entry(q, k, v, in_dtype, out, out_dtype, den_or_null, B, H, N, d, dv, scale, eps, normalize,
+                        workspace, workspace_bytes, hip_stream, 2);
 }
 
 size_t la_based_chunked_workspace_bytes(int B, int H, int N, int d, int dv, int chunk) {

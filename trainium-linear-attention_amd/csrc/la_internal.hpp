@@ -16,6 +16,7 @@ struct ParallelArgs {
   float* den;          // optional, (BH, N) fp32, den without eps
   void* workspace;     // optional scratch of parallel_workspace_bytes(); enables the packed path
   size_t workspace_bytes;
+  int stages;          // packed path: 1 = pre-pass (pack V), 2 = main kernel, 3 = both
   int BH, N, d, dv;
   float scale, eps;
   bool normalize;

@@ -34,6 +34,11 @@ _SIGNATURES = {
     "la_based_parallel_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_void,
                                        _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int,
                                        _c_void, _c_size, _c_void]),
+    "la_based_parallel_pack": (_c_int, [_c_void, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void, _c_size,
+                                        _c_void]),
+    "la_based_parallel_fwd_packed": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_void,
+                                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int,
+                                              _c_void, _c_size, _c_void]),
     "la_based_chunked_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "la_based_chunked_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
                                       _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int, _c_void,
