@@ -2,31 +2,36 @@
 //
 // Replaces the NKI chunked kernel (kernels/nki_attention_chunked.py:27-113) and the feature
 // map + padding of its wrapper (benchmarks/chunked_attention_benchmark.py:96-126).  The
-// recurrence is the reference's: per chunk c of 64 tokens,
+// recurrence is the reference's: per chunk c,
 //     out_c = phi(Q_c) S + causal(phi(Q_c) phi(K_c)^T) V_c,    S += phi(K_c)^T V_c,
 // extended with the K-sum z (den = phi(q).z + intra row sum) so it can also normalise.
 //
 // Design for MI355X:
-//   * phi is never materialised in HBM.  The Taylor features of q and k are formed in
-//     registers right before the MFMAs that consume them, from q~ = sqrt(c) q, k~ = sqrt(c) k.
-//   * Internal feature basis (160 features + the constant): 10 "slots" of 16,
-//       slot 0: q~_i (linear)          slot 1: q~_i^2 / 2 (q side) | k~_i^2 (k side)
-//       slot 2j, 2j+1 (j = 1..4): q~_i q~_{i+delta} (i + delta mod 16), delta = j and j + 4;
-//       delta = 8 visits every pair twice, so its k side carries a factor 1/2.
-//     With it, phi(q).phi(k) = 1 + s + s^2/2 exactly, and in every K-step of the
-//     phi(Q).S MFMA the lane groups that hold different slots run the same instructions on
-//     rotated copies of q~ (register indices are compile-time constants).
-//   * The constant feature is exact fp32: S_0 = sum v and z_0 = token count.
-//   * phi operands and the state operand are fp16 (the state itself accumulates in fp32 MFMA
-//     accumulators); q~ and k~ carry 2^(+-sigma/2) so the state stays well inside the fp16
-//     range for long sequences.  Intra-chunk terms use the d-form (q.k) exactly like the
-//     diagonal block of the parallel kernel (fp16 P, exact "1" through a mask MFMA).
-//   * Sequence parallelism: the sequence is cut into P segments.  Kernel 1 computes each
-//     segment's state increment (fp16 S, fp32 z and sum v) into the workspace; kernel 2 runs
-//     the chunk recurrence of every segment in parallel, starting from the sum of the
-//     increments of the earlier segments.  Within a work-group (4 waves) the state lives in
-//     registers: wave w owns slots {w, w+4, w+8} for all dv, and shares them with the other
-//     waves through LDS (fp16) once per chunk.
+//   * Every product runs on v_mfma_f32_32x32x16_f16 (the 16x16x32 forms issue at half the
+//     rate on gfx950).  Chunks are 128 tokens; wave w of a work-group owns query tokens
+//     32w .. 32w+31 of every chunk.
+//   * phi is never materialised in HBM.  With q~ = alpha q and k~ = beta k (alpha beta = scale)
+//     the kernel works in units of 2p:  2 p(s) = 2 + 2 s + s^2 = sum_f qf(q~) kf(k~), over 160
+//     feature slots (10 K-steps of 16) holding the 153 distinct features of the symmetric
+//     Taylor map: the constant, q~_i, q~_i^2 and q~_i q~_j (i < j).  The q side of a K-step is
+//     four packed-fp16 products of q~'s eight register pairs R_x = (q~_2x, q~_2x+1); the two
+//     lane halves of the MFMA operand hold q~ rotated by one register, so one v_pk_mul_f16
+//     yields two features for each half ("templates" below).  All coefficients live on the k
+//     side, which multiplies two rows of an LDS table [k~ | 2 k~ | 1 | 0 | 2] (K^T, token pairs
+//     packed), again one v_pk_mul_f16 per two products.
+//   * The state S (160 x dv, fp32 MFMA accumulators) stays in registers across chunks,
+//     partitioned over the waves by blocks of 32 features; every chunk it is published to LDS
+//     as fp16 S^T for the inter-chunk product phi(Q) S of all waves.
+//   * The k-sums z of all 153 features follow from the Gram matrix G = sum_u g_u g_u^T of
+//     g_u = [k~_u | 1] (17 x 17, one 32 x 32 accumulator, 8 MFMAs per chunk): the denominator of
+//     the earlier tokens is q'^T G q' + count with q' = [q~ | 1], two MFMAs per query tile.
+//   * Intra-chunk: scores 1 + q~.k~ on the same fp16 q~, k~ (one MFMA per 32 x 32 tile),
+//     P = b^2 + 1 = 2 p, masked on the diagonal tile, then P V on MFMA.  The score tile's key
+//     rows are permuted so that its accumulator layout is directly the B operand of P V.
+//   * Sequence parallelism: the sequence is cut into P segments of whole chunks.  Kernel 1
+//     computes every segment's state increment (fp16 S^T, fp32 G) into the workspace, kernel 2
+//     turns them into exclusive prefixes, kernel 3 runs the chunk recurrence of all segments
+//     in parallel from those prefixes.
 #include <math.h>
 
 #include "../../include/based_la.h"
@@ -37,24 +42,91 @@ namespace la {
 
 namespace {
 
-constexpr int CH = 64;          // tokens per chunk
-constexpr int NF = 160;         // internal features without the constant
-constexpr int NSLOT = 10;
-constexpr int DVC = 64;         // dv padded
-constexpr int STS = NF + 8;     // LDS row stride of S^T (fp16): 84 dwords, conflict-free 16 B reads
-constexpr int KTS = CH + 4;     // LDS row stride of k~^T (fp32)
-constexpr int VTS = CH + 8;     // LDS row stride of V^T (fp16): 16 B aligned rows
-constexpr int QKS = 16 + 8;     // LDS row stride of Q, K (bf16)
+constexpr int CH = 128;         // tokens per chunk
+constexpr int NF = 160;         // feature slots
+constexpr int QRS = 24;         // row stride (halves) of the q~ / k~ row tables: 48 B
+constexpr int KRS = 136;        // row stride (halves) of the K^T and V^T tables: 272 B
+constexpr int STS = 168;        // row stride (halves) of S^T: 336 B
+constexpr int KT_ROWS = 36;
+constexpr int R_ONES = 32, R_ZA = 33, R_ZB = 34, R_TWOS = 35;   // constant rows of K^T
+constexpr int NWAVE_OUT = 4;
+constexpr int NWAVE_SEG = 5;
+constexpr int MAX_SEG = 32;
 
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f4;
-
-__device__ __forceinline__ f32x4 mfma16_f16(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
-                                                0);
+// ---- feature templates
+//
+// Slot f = 16 kk + 8 h + 2 m + e: K-step kk, lane half h, packed register m, half e.  The q side
+// of (kk, m) is template tpl(4 kk + m) applied to the register pairs R'_x = R_{(x + h) mod 8}:
+//   L a     : R'_a                        (q~_i)
+//   S a     : R'_a * R'_a                 (q~_i^2)
+//   X a     : R'_a * swap(R'_a)           (q~_2x q~_2x+1 in the low half; the high half
+//                                          duplicates it and is unused, except for a = 0 where
+//                                          it is replaced by 1: the constant feature)
+//   P a b s : R'_a * (s ? swap(R'_b) : R'_b)
+// The rotation by h makes every template cover two disjoint sets of registers, so the 40
+// templates hold each of the 153 features exactly once.  Templates of one K-step share the
+// type and use a = 0, 2, 4, 6, which keeps the k-side row reads of a K-step on distinct LDS
+// banks.
+enum { TL = 0, TS = 1, TX = 2, TP = 3 };
+struct Tpl {
+  int t, a, b, sw;
+};
+__host__ __device__ constexpr Tpl tpl(int i) {
+  const int kk = i >> 2, m = i & 3, a = 2 * m;
+  if (kk == 0) return Tpl{TL, a, 0, 0};
+  if (kk == 1) return Tpl{TS, a, 0, 0};
+  if (kk == 2) return Tpl{TX, a, 0, 0};
+  if (kk < 9) return Tpl{TP, a, (a + ((kk - 1) >> 1)) & 7, (kk - 1) & 1};
+  return m < 2 ? Tpl{TP, a, a + 4, 0} : Tpl{TP, a, a - 4, 1};   // register pairs 4 apart
 }
-__device__ __forceinline__ f32x4 mfma16_bf16(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
-                                                 0, 0);
+
+// k-side rows (K^T table rows multiplied together) of feature slot f.
+struct KRows {
+  int a, b;
+};
+__host__ __device__ constexpr KRows krows(int f) {
+  const int kk = f >> 4, h = (f >> 3) & 1, m = (f >> 1) & 3, e = f & 1;
+  const Tpl t = tpl(4 * kk + m);
+  const int x = (t.a + h) & 7, y = (t.b + h) & 7;
+  if (t.t == TL) return KRows{16 + 2 * x + e, R_ONES};
+  if (t.t == TS) return KRows{2 * x + e, 2 * x + e};
+  if (t.t == TX) {
+    if (e == 0) return KRows{2 * x, 16 + 2 * x + 1};
+    return (t.a == 0 && h == 0) ? KRows{R_TWOS, R_ONES} : KRows{R_ZA, R_ZB};
+  }
+  return KRows{2 * x + e, 16 + (t.sw ? 2 * y + 1 - e : 2 * y + e)};
+}
+
+// Reference feature (benchmarks/chunked_attention_benchmark.py:34-53 order: 1, x_i, x_i^2,
+// x_i x_j for i < j row-major) of slot f, and the factor from the internal k side to it as
+// an index into {1/2, 2^(sigma/2)/2, 2^sigma/sqrt 2, 2^sigma/2}; ref = -1 for unused slots.
+struct RefFeat {
+  int ref, fac;
+};
+__host__ __device__ constexpr RefFeat ref_feature(int f) {
+  const int kk = f >> 4, h = (f >> 3) & 1, m = (f >> 1) & 3, e = f & 1;
+  const Tpl t = tpl(4 * kk + m);
+  const int x = (t.a + h) & 7, y = (t.b + h) & 7;
+  int i = 0, j = 0;
+  if (t.t == TL) return RefFeat{1 + 2 * x + e, 1};
+  if (t.t == TS) return RefFeat{17 + 2 * x + e, 2};
+  if (t.t == TX) {
+    if (e == 1) return (t.a == 0 && h == 0) ? RefFeat{0, 0} : RefFeat{-1, 0};
+    i = 2 * x;
+    j = 2 * x + 1;
+  } else {
+    i = 2 * x + e;
+    j = t.sw ? 2 * y + 1 - e : 2 * y + e;
+  }
+  const int lo = i < j ? i : j, hi = i < j ? j : i;
+  return RefFeat{33 + lo * (31 - lo) / 2 + (hi - lo - 1), 3};
+}
+
+// Row order of a 32-row MFMA operand whose accumulator is reused as the next operand: C row
+// 8 jj + 4 h + i (lane half h) carries item perm32 = 16 (jj >> 1) + 8 h + 4 (jj & 1) + i, so
+// lane half h holds items 16 J + 8 h .. +7 in accumulator elements 8 J .. 8 J + 7.
+__host__ __device__ constexpr int perm32(int rho) {
+  return 16 * (rho >> 4) + 8 * ((rho >> 2) & 1) + 4 * ((rho >> 3) & 1) + (rho & 3);
 }
 
 struct ChunkParams {
@@ -63,17 +135,13 @@ struct ChunkParams {
   const uint16_t* v;
   void* out;
   float* state_out;
-  uint16_t* wsS;    // [BH][P][DVC][NF] fp16 segment increments of S (transposed, internal basis)
-  float* wsZ;       // [BH][P][NF]
-  float* wsV;       // [BH][P][DVC]  sum of v over the segment
+  uint16_t* wsS;    // [BH][P][64][NF] fp16 S^T increments, then prefixes
+  float* wsG;       // [BH][P][64 lanes][16] fp32 Gram increments (accumulator layout), then prefixes
   int BH, N, dv, P, seg_chunks;
-  float inv_c, inv_c2, fscale, eps;   // intra d-form constants (as in the parallel kernel)
-  float qscale;                       // 2^-k on q for the intra scores
-  float qphi, kphi;                   // q~ = qphi * q, k~ = kphi * k
-  float W;                            // weight of "1" in intra u units; q-side phi carries it too
-  float st_lin, st_diag, st_off;      // internal -> reference feature basis factors (state export)
-  u32 ones_hi, ones_lo;
-  int normalize, out_f32, vec, vec_out;   // vec_out: dv % 4 == 0 and out 16-byte aligned
+  float alpha, beta;                 // q~ = alpha q, k~ = beta k
+  float eps;
+  float st_fac[4];                   // internal -> reference feature factors (state export)
+  int normalize, out_f32, vec_out;
 };
 
 __device__ __forceinline__ void map_segment(int wg, int BH, int P, int& bh, int& p) {
@@ -88,607 +156,699 @@ __device__ __forceinline__ void map_segment(int wg, int BH, int P, int& bh, int&
   }
 }
 
-// Shared-memory image of one chunk.
-struct ChunkLds {
-  uint16_t Qs[CH * QKS];     // bf16 row-major
-  uint16_t Ks[CH * QKS];     // bf16 row-major
-  float KT[16 * KTS];        // k~^T fp32
-  uint16_t VT[DVC * VTS];    // V^T fp16
-  uint16_t ST[DVC * STS];    // S^T fp16 (internal basis, scaled by W on use)
-  float Z[NF];               // z (internal basis) fp32
-  float S0[DVC];             // sum of v over all earlier tokens, fp32
-  float S0c[DVC];            // sum of v over this chunk
+constexpr int GRS = 40;   // row stride (halves) of the fp16 Gram matrix in LDS: 80 B
+
+// LDS image of one chunk and of the published state.
+struct OutLds {
+  uint16_t Q0[CH * QRS];        // q~ rows (fp16)
+  uint16_t Q1[CH * QRS];        // q~ rows rotated left by two elements
+  uint16_t Kr[CH * QRS];        // k~ rows
+  uint16_t KT[KT_ROWS * KRS];   // k~^T, (2 k~)^T, constant rows
+  uint16_t VT[64 * KRS];        // V^T
+  uint16_t ST[64 * STS];        // S^T (feature slots)
+  uint16_t G16[32 * GRS];       // Gram matrix [k~ | 1]^T [k~ | 1] of earlier tokens, (16,16) zeroed
+};
+struct SegTables {
+  uint16_t KT[KT_ROWS * KRS];
+  uint16_t VT[64 * KRS];
+};
+struct SegLds {
+  SegTables buf[2];
 };
 
-// Registers that carry one chunk from global memory to LDS.
-struct ChunkRegs {
-  u32x4 qk;          // threads 0..127: q rows, 128..255: k rows (16 B each)
-  u32x2 v[4];        // 4 tokens x 4 dv of V
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0); global loads and stores stay in flight
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ u32 swap16(u32 x) { return __builtin_amdgcn_alignbit(x, x, 16); }
+
+// Constant rows of the K^T table (written once per kernel).
+__device__ __forceinline__ void init_kt_constants(uint16_t* KT, int tid, int nthreads) {
+  for (int i = tid; i < 4 * (CH / 2); i += nthreads) {
+    const int row = R_ONES + (i >> 6), col = 2 * (i & 63);
+    const u32 val = row == R_ONES ? 0x3c003c00u : (row == R_TWOS ? 0x40004000u : 0u);
+    *reinterpret_cast<u32*>(&KT[row * KRS + col]) = val;
+  }
+}
+
+// K^T row holding component rho of g_u = [k~_u | 1 | 0 ...] (the Gram operand).
+__device__ __forceinline__ int gram_row(int rho) { return rho < 16 ? rho : (rho == 16 ? R_ONES : R_ZA); }
+
+// ---- staging: global -> registers -> (convert) -> LDS
+//
+// Wave wv (0..3) stages q, k dims 4 wv .. +3 and v dims 16 wv .. +15; lane l the token pair
+// 2l, 2l + 1 of the chunk, so that every LDS store instruction writes consecutive dwords of one
+// table row.
+struct StageRegs {
+  u32x2 q[2], k[2];
+  u32x4 v[2][2];
 };
 
-// QK: load q (threads 0..127) and k (128..255); otherwise only k (threads 0..127).
-template <bool VEC, bool QK>
-__device__ __forceinline__ void chunk_load(ChunkRegs& r, const ChunkParams& p, const uint16_t* qg, const uint16_t* kg,
-                                           const uint16_t* vg, int row0, int tid) {
+template <bool VEC_V, bool WITH_Q>
+__device__ __forceinline__ void stage_load(StageRegs& s, const ChunkParams& p, const uint16_t* qh,
+                                           const uint16_t* kh, const uint16_t* vh, int row0, int l, int wv) {
   const int N = p.N, dv = p.dv;
-  {
-    const int t = tid & 127, row = row0 + (t >> 1), col = 8 * (t & 1);
-    const uint16_t* base = QK ? ((tid < 128) ? qg : kg) : kg;
-    u32x4 x = {0u, 0u, 0u, 0u};
-    if (row < N && (QK || tid < 128)) {
-      const uint16_t* src = base + (size_t)row * 16 + col;
-      if (VEC) {
-        x = *reinterpret_cast<const u32x4*>(src);
-      } else {
+  const u32 rem = (u32)(N - row0);   // > 0
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kh + (size_t)row0 * 16, rem * 32u);
+  __amdgpu_buffer_rsrc_t rq = rk;
+  if (WITH_Q) rq = make_rsrc(qh + (size_t)row0 * 16, rem * 32u);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int voff = (2 * l + j) * 32 + 8 * wv;
+    if (WITH_Q) s.q[j] = buf_load_b64(rq, voff);
+    s.k[j] = buf_load_b64(rk, voff);
+  }
+  if (VEC_V) {
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vh + (size_t)row0 * dv, rem * (u32)dv * 2u);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int hv = 0; hv < 2; ++hv) {
+        const int col = 16 * wv + 8 * hv;
+        const int voff = col < dv ? ((2 * l + j) * dv + col) * 2 : kOffOutOfRange;
+        s.v[j][hv] = buf_load_b128(rv, voff);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int row = row0 + 2 * l + j;
+#pragma unroll
+      for (int hv = 0; hv < 2; ++hv) {
+        const int col = 16 * wv + 8 * hv;
         uint16_t e[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = src[i];
-        x = (u32x4){e[0] | ((u32)e[1] << 16), e[2] | ((u32)e[3] << 16), e[4] | ((u32)e[5] << 16),
-                    e[6] | ((u32)e[7] << 16)};
-      }
-    }
-    r.qk = x;
-  }
-  {
-    const int g4 = tid & 15, kg4 = tid >> 4, col = 4 * g4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = row0 + 4 * kg4 + i;
-      u32x2 x = {0u, 0u};
-      if (row < N && col < dv) {
-        const uint16_t* src = vg + (size_t)row * dv + col;
-        if (VEC) {
-          x = *reinterpret_cast<const u32x2*>(src);
-        } else {
-          uint16_t e[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) e[t] = (col + t < dv) ? src[t] : (uint16_t)0;
-          x = (u32x2){e[0] | ((u32)e[1] << 16), e[2] | ((u32)e[3] << 16)};
-        }
-      }
-      r.v[i] = x;
-    }
-  }
-}
-
-template <bool QK>
-__device__ __forceinline__ void chunk_store(const ChunkRegs& r, ChunkLds& L, float kphi, int tid) {
-  {
-    const int t = tid & 127, row = t >> 1, col = 8 * (t & 1);
-    if (QK && tid < 128) {
-      *reinterpret_cast<u32x4*>(&L.Qs[row * QKS + col]) = r.qk;
-    } else if (QK || tid < 128) {
-      if (QK) *reinterpret_cast<u32x4*>(&L.Ks[row * QKS + col]) = r.qk;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        L.KT[(col + 2 * e) * KTS + row] = kphi * bf16_lo_to_f32(r.qk[e]);
-        L.KT[(col + 2 * e + 1) * KTS + row] = kphi * bf16_hi_to_f32(r.qk[e]);
+        for (int i = 0; i < 8; ++i) e[i] = (row < N && col + i < dv) ? vh[(size_t)row * dv + col + i] : (uint16_t)0;
+        s.v[j][hv] = (u32x4){e[0] | ((u32)e[1] << 16), e[2] | ((u32)e[3] << 16), e[4] | ((u32)e[5] << 16),
+                             e[6] | ((u32)e[7] << 16)};
       }
     }
   }
-  {
-    const int g4 = tid & 15, kg4 = tid >> 4;
-    const u32 a0 = r.v[0][0], a1 = r.v[1][0], a2 = r.v[2][0], a3 = r.v[3][0];
-    const u32 b0 = r.v[0][1], b1 = r.v[1][1], b2 = r.v[2][1], b3 = r.v[3][1];
-    const u32x2 c0 = {pack_f16x2(bf16_lo_to_f32(a0), bf16_lo_to_f32(a1)), pack_f16x2(bf16_lo_to_f32(a2), bf16_lo_to_f32(a3))};
-    const u32x2 c1 = {pack_f16x2(bf16_hi_to_f32(a0), bf16_hi_to_f32(a1)), pack_f16x2(bf16_hi_to_f32(a2), bf16_hi_to_f32(a3))};
-    const u32x2 c2 = {pack_f16x2(bf16_lo_to_f32(b0), bf16_lo_to_f32(b1)), pack_f16x2(bf16_lo_to_f32(b2), bf16_lo_to_f32(b3))};
-    const u32x2 c3 = {pack_f16x2(bf16_hi_to_f32(b0), bf16_hi_to_f32(b1)), pack_f16x2(bf16_hi_to_f32(b2), bf16_hi_to_f32(b3))};
-    uint16_t* dst = &L.VT[(4 * g4) * VTS + 4 * kg4];
-    *reinterpret_cast<u32x2*>(dst) = c0;
-    *reinterpret_cast<u32x2*>(dst + VTS) = c1;
-    *reinterpret_cast<u32x2*>(dst + 2 * VTS) = c2;
-    *reinterpret_cast<u32x2*>(dst + 3 * VTS) = c3;
-  }
 }
 
-// delta (pair offset) of a slot on the k side, and its extra factor
-__device__ __forceinline__ int slot_delta(int s) { return s < 2 ? 0 : ((s & 1) ? (s >> 1) + 4 : (s >> 1)); }
+// Converted staging values of one thread: fp16 q~ / k~ row pieces, k~ and 2 k~ token pairs of
+// dims 4 wv + i, V^T token pairs of dims 16 wv + 2 i (+1).
+struct StageConv {
+  u32 q[2][2], kr[2][2];
+  u32 kt[4], kt2[4];
+  u32 vt[16];
+};
 
-// A fragment (16 features x 32 tokens) of phi(K)^T for slot s, K-step ks: lane (feature row
-// r = l%16, group g) holds phi_{s,r}(k_u) for tokens u = 32ks + 8g .. +7, as fp16.
-__device__ __forceinline__ u32x4 phi_k_frag(const ChunkLds& L, int s, int ks, int r, int g) {
-  const float* a = &L.KT[r * KTS + 32 * ks + 8 * g];
-  const f4 a0 = *reinterpret_cast<const f4*>(a), a1 = *reinterpret_cast<const f4*>(a + 4);
-  float x[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-  if (s == 0) {
-    // linear: k~_r
-  } else if (s == 1) {
+template <bool WITH_Q>
+__device__ __forceinline__ void stage_convert(const StageRegs& s, StageConv& o, float alpha, float beta) {
+  if (WITH_Q) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = x[e] * x[e];
-  } else {
-    const int dl = slot_delta(s);
-    const float* b = &L.KT[((r + dl) & 15) * KTS + 32 * ks + 8 * g];
-    const f4 b0 = *reinterpret_cast<const f4*>(b), b1 = *reinterpret_cast<const f4*>(b + 4);
-    const float y[8] = {b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-    const float f = (dl == 8) ? 0.5f : 1.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = x[e] * (y[e] * f);
+    for (int j = 0; j < 2; ++j) {
+      o.q[j][0] = pack_f16x2(alpha * bf16_lo_to_f32(s.q[j][0]), alpha * bf16_hi_to_f32(s.q[j][0]));
+      o.q[j][1] = pack_f16x2(alpha * bf16_lo_to_f32(s.q[j][1]), alpha * bf16_hi_to_f32(s.q[j][1]));
+    }
   }
-  return (u32x4){pack_f16x2(x[0], x[1]), pack_f16x2(x[2], x[3]), pack_f16x2(x[4], x[5]), pack_f16x2(x[6], x[7])};
-}
-
-// State update for the slots a wave owns: S[slot][nt] += phi(K)^T V (all dv), z[slot] += sum
-// over tokens of phi(K).  S: accumulators (rows = features 4g+i, col = dv 16nt + l%16).
-template <int NS>
-__device__ __forceinline__ void update_slots(const ChunkLds& L, f32x4 (&S)[3][4], float (&z)[3], int w, int lane) {
-  const int r = lane & 15, g = lane >> 4;
-  constexpr u32 kOnes = 0x3c003c00u;
+  float kf[2][4];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    u32x4 vb[4];
+  for (int j = 0; j < 2; ++j) {
+    kf[j][0] = beta * bf16_lo_to_f32(s.k[j][0]);
+    kf[j][1] = beta * bf16_hi_to_f32(s.k[j][0]);
+    kf[j][2] = beta * bf16_lo_to_f32(s.k[j][1]);
+    kf[j][3] = beta * bf16_hi_to_f32(s.k[j][1]);
+    if (WITH_Q) {
+      o.kr[j][0] = pack_f16x2(kf[j][0], kf[j][1]);
+      o.kr[j][1] = pack_f16x2(kf[j][2], kf[j][3]);
+    }
+  }
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-      vb[nt] = *reinterpret_cast<const u32x4*>(&L.VT[(16 * nt + r) * VTS + 32 * ks + 8 * g]);
+  for (int i = 0; i < 4; ++i) {
+    o.kt[i] = pack_f16x2(kf[0][i], kf[1][i]);   // (token 2l, token 2l+1) of dim 4wv+i
+    o.kt2[i] = pk_mul_f16(o.kt[i], 0x40004000u);
+  }
 #pragma unroll
-    for (int j = 0; j < NS; ++j) {
-      const int s = w + 4 * j;
-      const u32x4 a = phi_k_frag(L, s, ks, r, g);
-      float zz = z[j];
-      zz = dot2_f16(a[0], kOnes, zz);
-      zz = dot2_f16(a[1], kOnes, zz);
-      zz = dot2_f16(a[2], kOnes, zz);
-      zz = dot2_f16(a[3], kOnes, zz);
-      z[j] = zz;
+  for (int hv = 0; hv < 2; ++hv) {
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) S[j][nt] = mfma16_f16(a, vb[nt], S[j][nt]);
+    for (int w = 0; w < 4; ++w) {
+      const u32 a = s.v[0][hv][w], b = s.v[1][hv][w];
+      o.vt[2 * (4 * hv + w)] = pack_f16x2(bf16_lo_to_f32(a), bf16_lo_to_f32(b));
+      o.vt[2 * (4 * hv + w) + 1] = pack_f16x2(bf16_hi_to_f32(a), bf16_hi_to_f32(b));
     }
   }
 }
 
-// Column sums of V over this chunk (fp16 V exact, fp32 sums) into L.S0c; threads 0..255:
-// dv row tid/4, token quarter tid%4.
-__device__ __forceinline__ float chunk_vsum_part(const ChunkLds& L, int tid) {
-  constexpr u32 kOnes = 0x3c003c00u;
-  const uint16_t* src = &L.VT[(tid >> 2) * VTS + 16 * (tid & 3)];
-  const u32x4 a = *reinterpret_cast<const u32x4*>(src), b = *reinterpret_cast<const u32x4*>(src + 8);
-  float s = 0.f;
+// Keeps the conversion above this point (the compiler would otherwise sink it next to the LDS
+// stores, between two barriers where every wave waits for it).
+template <bool WITH_Q>
+__device__ __forceinline__ void stage_pin(StageConv& o) {
+  if (WITH_Q) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) s = dot2_f16(a[e], kOnes, s);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) s = dot2_f16(b[e], kOnes, s);
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  return s;   // full chunk sum of dv row tid/4, in every lane of the quad
-}
-
-// Reduces a per-lane partial over the 4 lane groups (lanes l, l^16, l^32, l^48).
-__device__ __forceinline__ float sum_groups(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
-}
-
-// Writes the wave's slots of S (fp16, transposed) and z into LDS.  z[j] holds per-lane partial
-// sums (row r = lane % 16, split over the 4 lane groups).
-template <int NS>
-__device__ __forceinline__ void publish_slots(ChunkLds& L, const f32x4 (&S)[3][4], const float (&z)[3], int w, int lane) {
-  const int r = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int j = 0; j < NS; ++j) {
-    const int s = w + 4 * j;
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const u32x2 pk = {pack_f16x2(S[j][nt][0], S[j][nt][1]), pack_f16x2(S[j][nt][2], S[j][nt][3])};
-      *reinterpret_cast<u32x2*>(&L.ST[(16 * nt + r) * STS + 16 * s + 4 * g]) = pk;
-    }
-    const float zt = sum_groups(z[j]);
-    if (g == 0) L.Z[16 * s + r] = zt;
+    for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(o.q[j][0]), "+v"(o.q[j][1]), "+v"(o.kr[j][0]), "+v"(o.kr[j][1]));
   }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(o.kt[i]), "+v"(o.kt2[i]));
+#pragma unroll
+  for (int i = 0; i < 16; i += 4) asm volatile("" : "+v"(o.vt[i]), "+v"(o.vt[i + 1]), "+v"(o.vt[i + 2]), "+v"(o.vt[i + 3]));
+}
+
+template <bool WITH_Q>
+__device__ __forceinline__ void stage_write(const StageConv& o, uint16_t* Q0, uint16_t* Q1, uint16_t* Kr,
+                                            uint16_t* KT, uint16_t* VT, int l, int wv) {
+  const int dq = wv;
+  if (WITH_Q) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int tok = 2 * l + j;
+      *reinterpret_cast<u32x2*>(&Q0[tok * QRS + 4 * dq]) = (u32x2){o.q[j][0], o.q[j][1]};
+      // rotated copy: element i of Q1 is element (i + 2) mod 16 of q~
+      *reinterpret_cast<u32*>(&Q1[tok * QRS + ((4 * dq + 14) & 15)]) = o.q[j][0];
+      *reinterpret_cast<u32*>(&Q1[tok * QRS + 4 * dq]) = o.q[j][1];
+      *reinterpret_cast<u32x2*>(&Kr[tok * QRS + 4 * dq]) = (u32x2){o.kr[j][0], o.kr[j][1]};
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    *reinterpret_cast<u32*>(&KT[(4 * dq + i) * KRS + 2 * l]) = o.kt[i];
+    *reinterpret_cast<u32*>(&KT[(16 + 4 * dq + i) * KRS + 2 * l]) = o.kt2[i];
+  }
+  // V^T: row c = 16 dq + 2 i (+1), token pair l
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    *reinterpret_cast<u32*>(&VT[(16 * dq + 2 * i) * KRS + 2 * l]) = o.vt[2 * i];
+    *reinterpret_cast<u32*>(&VT[(16 * dq + 2 * i + 1) * KRS + 2 * l]) = o.vt[2 * i + 1];
+  }
+}
+
+// ---- state update of NB blocks of 32 feature slots over one chunk (all dv)
+//
+// A = phi(K)^T tile (32 slots x 16 tokens): lane (row r, tokens 8h .. +7 of the K-step) forms
+// its slot's product of two K^T rows; B = V (16 tokens x 32 dv) from V^T.
+template <int NB>
+__device__ __forceinline__ void update_blocks(const uint16_t* KT, const uint16_t* VT, f32x16 (&S)[NB][2],
+                                              const int (&ra)[NB], const int (&rb)[NB], int r, int h) {
+#pragma unroll
+  for (int s = 0; s < CH / 16; ++s) {
+    u32x4 bv[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) bv[n] = *reinterpret_cast<const u32x4*>(&VT[(32 * n + r) * KRS + 16 * s + 8 * h]);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const u32x4 x = *reinterpret_cast<const u32x4*>(&KT[ra[b] + 16 * s + 8 * h]);
+      const u32x4 y = *reinterpret_cast<const u32x4*>(&KT[rb[b] + 16 * s + 8 * h]);
+      u32x4 a;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = pk_mul_f16(x[i], y[i]);
+#pragma unroll
+      for (int n = 0; n < 2; ++n) S[b][n] = mfma32x32x16_f16(a, bv[n], S[b][n]);
+    }
+  }
+}
+
+// Gram matrix G += sum_u g_u g_u^T over the K-steps s of the chunk with (s % step) == first.
+__device__ __forceinline__ void gram_update(const uint16_t* KT, f32x16& G, int grow, int h, int first, int step) {
+  for (int s = first; s < CH / 16; s += step) {
+    const u32x4 x = *reinterpret_cast<const u32x4*>(&KT[grow + 16 * s + 8 * h]);
+    G = mfma32x32x16_f16(x, x, G);
+  }
+}
+
+// Slot of row r of the update tile of block b.
+__device__ __forceinline__ int block_slot(int b, int r) { return 32 * b + perm32(r); }
+
+// Gram coordinate and factor of a K^T row: z_f = fa fb G[da][db] for slot rows (a, b).
+__device__ __forceinline__ void kt_row_dim(int row, int& d, float& f) {
+  if (row < 16) { d = row; f = 1.f; }
+  else if (row < 32) { d = row - 16; f = 2.f; }
+  else if (row == R_ONES) { d = 16; f = 1.f; }
+  else if (row == R_TWOS) { d = 16; f = 2.f; }
+  else { d = 0; f = 0.f; }
 }
 
 // -------------------------------------------------------------------------------------------
-// Kernel 1: per (head, segment < P-1) state increment of the segment.
-template <bool VEC>
-__global__ __launch_bounds__(256, 2) void chunked_segment_kernel(const ChunkParams p) {
-  __shared__ __attribute__((aligned(16))) ChunkLds L;
+// Kernel 1: state increment of every segment but the last.  Work-group (head, segment); wave w
+// owns feature block w (all dv) and K-steps w, w + 5 of the Gram matrix; waves 0..3 stage.
+template <bool VEC_V>
+__global__ __launch_bounds__(64 * NWAVE_SEG) void chunked_segment_kernel(const ChunkParams p) {
+  __shared__ __attribute__((aligned(16))) SegLds L;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, h = lane >> 5;
   int bh, seg;
   map_segment(blockIdx.x, p.BH, p.P - 1, bh, seg);
   const size_t hrow = (size_t)bh * p.N;
-  const uint16_t* qg = p.q + hrow * 16;
-  const uint16_t* kg = p.k + hrow * 16;
-  const uint16_t* vg = p.v + hrow * p.dv;
-  const int c0 = seg * p.seg_chunks;
-  const int nch = p.seg_chunks;
+  const uint16_t* kh = p.k + hrow * 16;
+  const uint16_t* vh = p.v + hrow * p.dv;
+  const int c0 = seg * p.seg_chunks, nch = p.seg_chunks;
+  const bool stager = w < 4;
 
-  f32x4 S[3][4];
-  float z[3];
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    z[j] = 0.f;
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) S[j][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  }
-  float vs = 0.f;
+  const KRows kr = krows(block_slot(w, r));
+  const int ra[1] = {kr.a * KRS}, rb[1] = {kr.b * KRS};
+  const int grow = gram_row(r) * KRS;
+  f32x16 S[1][2] = {{splat16(0.f), splat16(0.f)}};
+  f32x16 G = splat16(0.f);
 
-  // two chunks in flight: chunk c is stored from its registers, then chunk c + 2 is loaded into them
-  ChunkRegs ra, rb;
-  chunk_load<VEC, false>(ra, p, qg, kg, vg, c0 * CH, tid);
-  if (nch > 1) chunk_load<VEC, false>(rb, p, qg, kg, vg, (c0 + 1) * CH, tid);
-  auto step = [&](ChunkRegs& cur, int c) {
-    __syncthreads();   // previous chunk fully consumed
-    chunk_store<false>(cur, L, p.kphi, tid);
-    __syncthreads();
-    if (c + 2 < nch) chunk_load<VEC, false>(cur, p, qg, kg, vg, (c0 + c + 2) * CH, tid);
-    if (w < 2)
-      update_slots<3>(L, S, z, w, lane);
-    else
-      update_slots<2>(L, S, z, w, lane);
-    vs += chunk_vsum_part(L, tid);
-  };
-  for (int c = 0; c < nch; c += 2) {
-    step(ra, c);
-    if (c + 1 < nch) step(rb, c + 1);
+  init_kt_constants(L.buf[0].KT, tid, 64 * NWAVE_SEG);
+  init_kt_constants(L.buf[1].KT, tid, 64 * NWAVE_SEG);
+  StageRegs st;
+  StageConv cv;
+  if (stager) {
+    stage_load<VEC_V, false>(st, p, nullptr, kh, vh, c0 * CH, lane, w);
+    stage_convert<false>(st, cv, p.alpha, p.beta);
+    stage_write<false>(cv, nullptr, nullptr, nullptr, L.buf[0].KT, L.buf[0].VT, lane, w);
   }
-  // write the increment: S^T fp16 [dv][f], z, sum v
-  const int r = lane & 15, g = lane >> 4;
-  const size_t sidx = (size_t)bh * p.P + seg;
-  uint16_t* wsS = p.wsS + sidx * (DVC * NF);
-  const int NS = w < 2 ? 3 : 2;
-#pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    if (j >= NS) break;
-    const int s = w + 4 * j;
-    float zz = sum_groups(z[j]);
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) {
-      const u32x2 pk = {pack_f16x2(S[j][nt][0], S[j][nt][1]), pack_f16x2(S[j][nt][2], S[j][nt][3])};
-      *reinterpret_cast<u32x2*>(&wsS[(16 * nt + r) * NF + 16 * s + 4 * g]) = pk;
+  lds_barrier();
+  for (int c = 0; c < nch; ++c) {
+    const SegTables& T = L.buf[c & 1];
+    if (stager && c + 1 < nch) stage_load<VEC_V, false>(st, p, nullptr, kh, vh, (c0 + c + 1) * CH, lane, w);
+    update_blocks<1>(T.KT, T.VT, S, ra, rb, r, h);
+    gram_update(T.KT, G, grow, h, w, NWAVE_SEG);
+    if (stager && c + 1 < nch) {
+      SegTables& U = L.buf[(c + 1) & 1];
+      stage_convert<false>(st, cv, p.alpha, p.beta);
+      stage_pin<false>(cv);
+      stage_write<false>(cv, nullptr, nullptr, nullptr, U.KT, U.VT, lane, w);
     }
-    if (g == 0) p.wsZ[sidx * NF + 16 * s + r] = zz;
+    lds_barrier();
   }
-  if ((tid & 3) == 0) p.wsV[sidx * DVC + (tid >> 2)] = vs;
+  // increment: S^T fp16 [dv][slot]; Gram partials of the waves summed through LDS
+  const size_t slot = (size_t)bh * p.P + seg;
+  uint16_t* ws = p.wsS + slot * (64 * NF);
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+#pragma unroll
+    for (int J = 0; J < 2; ++J) {
+      const f32x16& a = S[0][n];
+      const u32x4 pk = {pack_f16x2(a[8 * J + 0], a[8 * J + 1]), pack_f16x2(a[8 * J + 2], a[8 * J + 3]),
+                        pack_f16x2(a[8 * J + 4], a[8 * J + 5]), pack_f16x2(a[8 * J + 6], a[8 * J + 7])};
+      *reinterpret_cast<u32x4*>(&ws[(32 * n + r) * NF + 32 * w + 16 * J + 8 * h]) = pk;
+    }
+  }
+  float* red = reinterpret_cast<float*>(&L);   // 5 x 64 x 16 floats = 20 KB, tables no longer read
+#pragma unroll
+  for (int e = 0; e < 16; e += 4)
+    *reinterpret_cast<f32x4*>(&red[(w * 64 + lane) * 16 + e]) = (f32x4){G[e], G[e + 1], G[e + 2], G[e + 3]};
+  lds_barrier();
+  if (w == 0) {
+    float* gout = p.wsG + slot * 1024 + lane * 16;
+#pragma unroll
+    for (int e = 0; e < 16; e += 4) {
+      f32x4 acc = *reinterpret_cast<const f32x4*>(&red[lane * 16 + e]);
+#pragma unroll
+      for (int ww = 1; ww < NWAVE_SEG; ++ww) acc += *reinterpret_cast<const f32x4*>(&red[(ww * 64 + lane) * 16 + e]);
+      *reinterpret_cast<f32x4*>(&gout[e]) = acc;
+    }
+  }
 }
 
 // -------------------------------------------------------------------------------------------
-// Kernel 1b: inclusive prefix over segments, in place.  Thread (head, element); after it, slot
-// p - 1 holds sum_{p' < p} of the increments (S as fp16, z and sum v as fp32).  Values are read
-// 16 segments at a time with all loads in flight before the first store.
-template <class T>
-__device__ __forceinline__ float to_f(T x) {
-  if constexpr (sizeof(T) == 2) return (float)__builtin_bit_cast(_Float16, x);
-  else return x;
-}
-template <class T>
-__device__ __forceinline__ T from_f(float x) {
-  if constexpr (sizeof(T) == 2) return __builtin_bit_cast(uint16_t, (_Float16)x);
-  else return x;
-}
-template <class T>
-__device__ __forceinline__ void prefix_scan(T* base, size_t stride, int nseg) {
-  float acc = 0.f;
-  for (int s0 = 0; s0 < nseg; s0 += 16) {
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = s0 + i < nseg ? to_f(base[(size_t)(s0 + i) * stride]) : 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      acc += x[i];
-      if (s0 + i < nseg) base[(size_t)(s0 + i) * stride] = from_f<T>(acc);
-    }
-  }
-}
+// Kernel 2: exclusive prefixes over segments, in place: afterwards slot p - 1 holds the sum of
+// the increments of segments 0 .. p-1.  Thread (head, 16-byte unit); fp32 accumulation.
 __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p) {
-  constexpr int NS_ELEM = DVC * NF, NE = NS_ELEM + NF + DVC;
-  const int e = blockIdx.x * 256 + threadIdx.x;
-  const int bh = blockIdx.y;
-  if (e >= NE) return;
+  constexpr int US = 64 * NF / 8, UG = 1024 / 4;   // 16-byte units of S^T (fp16) and G (fp32)
+  const int e = blockIdx.x * 256 + threadIdx.x, bh = blockIdx.y;
   const int nseg = p.P - 1;
-  if (e < NS_ELEM)
-    prefix_scan(p.wsS + (size_t)bh * p.P * NS_ELEM + e, NS_ELEM, nseg);
-  else if (e < NS_ELEM + NF)
-    prefix_scan(p.wsZ + (size_t)bh * p.P * NF + (e - NS_ELEM), NF, nseg);
-  else
-    prefix_scan(p.wsV + (size_t)bh * p.P * DVC + (e - NS_ELEM - NF), DVC, nseg);
+  if (e < US) {
+    uint16_t* base = p.wsS + (size_t)bh * p.P * (64 * NF) + 8 * (size_t)e;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < nseg; s0 += 8) {
+      u32x4 x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        x[i] = s0 + i < nseg ? *reinterpret_cast<const u32x4*>(base + (size_t)(s0 + i) * (64 * NF))
+                             : (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (s0 + i >= nseg) break;
+        u32x4 o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[2 * j] += f16_lo_to_f32(x[i][j]);
+          acc[2 * j + 1] += f16_hi_to_f32(x[i][j]);
+          o[j] = pack_f16x2(acc[2 * j], acc[2 * j + 1]);
+        }
+        *reinterpret_cast<u32x4*>(base + (size_t)(s0 + i) * (64 * NF)) = o;
+      }
+    }
+  } else if (e < US + UG) {
+    float* base = p.wsG + (size_t)bh * p.P * 1024 + 4 * (size_t)(e - US);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < nseg; s0 += 8) {
+      f32x4 x[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        x[i] = s0 + i < nseg ? *reinterpret_cast<const f32x4*>(base + (size_t)(s0 + i) * 1024)
+                             : (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (s0 + i >= nseg) break;
+        acc += x[i];
+        *reinterpret_cast<f32x4*>(base + (size_t)(s0 + i) * 1024) = acc;
+      }
+    }
+  }
 }
 
 // -------------------------------------------------------------------------------------------
-// Kernel 2: outputs.  Work-group (head, segment); wave w handles tokens 16w..16w+15 of every
-// chunk for the phi(Q).S and intra terms, and owns state slots {w, w+4, w+8}.
-template <bool VEC, bool UNIT>
-__global__ __launch_bounds__(256, 2) void chunked_output_kernel(const ChunkParams p) {
-  __shared__ __attribute__((aligned(16))) ChunkLds L;
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 15, g = lane >> 4;
-  int bh, seg;
-  map_segment(blockIdx.x, p.BH, p.P, bh, seg);
+// Kernel 3: outputs.  Work-group (head, segment), 4 waves; wave W owns query tokens 32W .. +31
+// of each chunk and state blocks {0, 1} (W = 0) or {W + 1}; wave 1 also keeps the Gram matrix.
+template <int W>
+struct OwnedBlocks {
+  static constexpr int NB = W == 0 ? 2 : 1;
+  static constexpr int first = W == 0 ? 0 : W + 1;
+};
+constexpr int kGramWave = 1;
+
+template <int NB>
+__device__ __forceinline__ void publish_state(OutLds& L, const f32x16 (&S)[NB][2], int first, int r, int h) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int blk = first + b;
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+#pragma unroll
+      for (int J = 0; J < 2; ++J) {
+        const f32x16& a = S[b][n];
+        const u32x4 pk = {pack_f16x2(a[8 * J + 0], a[8 * J + 1]), pack_f16x2(a[8 * J + 2], a[8 * J + 3]),
+                          pack_f16x2(a[8 * J + 4], a[8 * J + 5]), pack_f16x2(a[8 * J + 6], a[8 * J + 7])};
+        *reinterpret_cast<u32x4*>(&L.ST[(32 * n + r) * STS + 32 * blk + 16 * J + 8 * h]) = pk;
+      }
+    }
+  }
+}
+
+// fp16 Gram matrix for the denominator, with the token count G(16,16) left out (it is added
+// exactly).  Lane (col j = r, rows 8 jj + 4 h + i) writes row j by symmetry.
+__device__ __forceinline__ void publish_gram(OutLds& L, const f32x16& G, int r, int h) {
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    float g0 = G[4 * jj], g1 = G[4 * jj + 1], g2 = G[4 * jj + 2], g3 = G[4 * jj + 3];
+    if (jj == 2 && h == 0 && r == 16) g0 = 0.f;
+    *reinterpret_cast<u32x2*>(&L.G16[r * GRS + 8 * jj + 4 * h]) = (u32x2){pack_f16x2(g0, g1), pack_f16x2(g2, g3)};
+  }
+}
+
+// VEC: v rows 16-byte aligned with dv % 8 == 0 and out 16-byte aligned with dv % 4 == 0 (buffer
+// loads and stores); otherwise element-wise accesses with bounds checks.
+template <int W, bool VEC, bool OUT_F32>
+__device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int bh, int seg) {
+  using OB = OwnedBlocks<W>;
+  constexpr int NB = OB::NB;
+  constexpr bool GRAM = W == kGramWave;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int r = lane & 31, h = lane >> 5;
   const int N = p.N, dv = p.dv;
   const size_t hrow = (size_t)bh * N;
-  const uint16_t* qg = p.q + hrow * 16;
-  const uint16_t* kg = p.k + hrow * 16;
-  const uint16_t* vg = p.v + hrow * dv;
+  const uint16_t* qh = p.q + hrow * 16;
+  const uint16_t* kh = p.k + hrow * 16;
+  const uint16_t* vh = p.v + hrow * dv;
   const int nchunks_total = (N + CH - 1) / CH;
   const int c0 = seg * p.seg_chunks;
   const int nch = min(p.seg_chunks, nchunks_total - c0);
-  const int NS = w < 2 ? 3 : 2;
-  const float W = p.W;
+  constexpr int esz = OUT_F32 ? 4 : 2;
 
-  // ---- state at the segment start: sum of the increments of earlier segments
-  f32x4 S[3][4];
-  float z[3];
+  // k-side rows of the owned slots
+  int ra[NB], rb[NB];
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    z[j] = 0.f;
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt) S[j][nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < NB; ++b) {
+    const KRows kr = krows(block_slot(OB::first + b, r));
+    ra[b] = kr.a * KRS;
+    rb[b] = kr.b * KRS;
   }
-  float s0 = 0.f;   // threads 0..63: sum of v over earlier segments for dv = tid
+  const int grow = gram_row(r) * KRS;
+  // causal mask of the diagonal score tile: element e of lane (query r, half h) is key
+  // 16 (e >> 3) + 8 h + (e & 7); packed pairs keep a half iff key <= r
+  u32 dmask[8];
+#pragma unroll
+  for (int x = 0; x < 8; ++x) {
+    const int k0 = 16 * ((2 * x) >> 3) + 8 * h + ((2 * x) & 7);
+    dmask[x] = (k0 <= r ? 0xffffu : 0u) | (k0 + 1 <= r ? 0xffff0000u : 0u);
+  }
+
+  // ---- state at the segment start
+  f32x16 S[NB][2];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    S[b][0] = splat16(0.f);
+    S[b][1] = splat16(0.f);
+  }
+  f32x16 G = splat16(0.f);
+  StageRegs st;
+  StageConv cv;
+  stage_load<VEC, true>(st, p, qh, kh, vh, c0 * CH, lane, W);
   if (seg > 0) {
-    // the prefix kernel left sum_{p' < seg} of the increments in slot seg - 1
-    const size_t sidx = (size_t)bh * p.P + (seg - 1);
-    const uint16_t* wsS = p.wsS + sidx * (DVC * NF);
+    const size_t slot = (size_t)bh * p.P + (seg - 1);
+    const uint16_t* ws = p.wsS + slot * (64 * NF);
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      if (j >= NS) break;
-      const int s = w + 4 * j;
+    for (int b = 0; b < NB; ++b) {
+      const int blk = OB::first + b;
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const u32x2 pk = *reinterpret_cast<const u32x2*>(&wsS[(16 * nt + r) * NF + 16 * s + 4 * g]);
-        S[j][nt][0] = f16_lo_to_f32(pk[0]);
-        S[j][nt][1] = f16_hi_to_f32(pk[0]);
-        S[j][nt][2] = f16_lo_to_f32(pk[1]);
-        S[j][nt][3] = f16_hi_to_f32(pk[1]);
+      for (int n = 0; n < 2; ++n) {
+#pragma unroll
+        for (int J = 0; J < 2; ++J) {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(&ws[(32 * n + r) * NF + 32 * blk + 16 * J + 8 * h]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            S[b][n][8 * J + 2 * i] = f16_lo_to_f32(x[i]);
+            S[b][n][8 * J + 2 * i + 1] = f16_hi_to_f32(x[i]);
+          }
+        }
       }
-      if (g == 0) z[j] = p.wsZ[sidx * NF + 16 * s + r];
     }
-    if (tid < DVC) s0 = p.wsV[sidx * DVC + tid];
-  }
-  // z partials are kept per lane group: group 0 holds the full value, others zero
-  if (w < 2)
-    publish_slots<3>(L, S, z, w, lane);
-  else
-    publish_slots<2>(L, S, z, w, lane);
-  if (tid < DVC) L.S0[tid] = s0;
+    if (GRAM) {
+      const float* gin = p.wsG + slot * 1024 + lane * 16;
 #pragma unroll
-  for (int j = 0; j < 3; ++j) z[j] = (g == 0) ? z[j] : 0.f;
+      for (int e = 0; e < 16; e += 4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(&gin[e]);
+        G[e] = x[0];
+        G[e + 1] = x[1];
+        G[e + 2] = x[2];
+        G[e + 3] = x[3];
+      }
+    }
+  }
 
-  const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
+  init_kt_constants(L.KT, tid, 64 * NWAVE_OUT);
+  publish_state<NB>(L, S, OB::first, r, h);
+  if (GRAM) publish_gram(L, G, r, h);
+  stage_convert<true>(st, cv, p.alpha, p.beta);
+  stage_write<true>(cv, L.Q0, L.Q1, L.Kr, L.KT, L.VT, lane, W);
+  lds_barrier();
+
   constexpr u32 kOnes = 0x3c003c00u;
-
-  ChunkRegs cur;
-  chunk_load<VEC, true>(cur, p, qg, kg, vg, c0 * CH, tid);
   for (int c = 0; c < nch; ++c) {
     const int row0 = (c0 + c) * CH;
-    __syncthreads();   // previous chunk consumed (Q, K, V, S^T, z, S0 readers done)
-    chunk_store<true>(cur, L, p.kphi, tid);
-    if (c > 0) {
-      if (w < 2)
-        publish_slots<3>(L, S, z, w, lane);
-      else
-        publish_slots<2>(L, S, z, w, lane);
-      if (tid < DVC) L.S0[tid] += L.S0c[tid];
-    }
-    __syncthreads();
-    if (c + 1 < nch) chunk_load<VEC, true>(cur, p, qg, kg, vg, row0 + CH, tid);
+    // next chunk (unconditional, which keeps the chunk body one basic block: past the end of the
+    // segment it reads the next segment's tokens or, past N, zeros, and the values go unused)
+    stage_load<VEC, true>(st, p, qh, kh, vh, min(row0 + CH, N - 1), lane, W);
 
-    // ---- q~ copies for this wave's token t = 16w + r (lane group g), rotated through the
-    // LDS address (no register-indexed selects):
-    //   xa[e] = q~[(e + 8*odd) % 16],  xb[e] = W * q~[(e + 8*odd + 4*hig) % 16],
-    //   xb0[e] = hig ? (W/2) xa[e] : W
-    const int tl = 16 * w + r;   // chunk-local token of this lane (A layout)
-    float xa[16], xb[16], xb0[16];
+    // ---- phi(q) of token 32W + r (lane half h: q~ rotated by 2h elements) and the
+    // inter-chunk product O^T += S^T phi(Q)^T
+    u32 R[8];
     {
-      const int odd = g & 1, hig = g >> 1;
-      const uint16_t* qrow = &L.Qs[tl * QKS];
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(qrow + 8 * odd);
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(qrow + 8 * (1 - odd));
-      const int rb = 8 * odd + 4 * hig;
-      u32x2 b[4];
+      const uint16_t* qrow = (h ? L.Q1 : L.Q0) + (32 * W + r) * QRS;
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(qrow);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(qrow + 8);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) b[t] = *reinterpret_cast<const u32x2*>(qrow + ((rb + 4 * t) & 15));
-      const float qp = p.qphi, qw = p.qphi * W;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xa[2 * e] = qp * bf16_lo_to_f32(a0[e]);
-        xa[2 * e + 1] = qp * bf16_hi_to_f32(a0[e]);
-        xa[8 + 2 * e] = qp * bf16_lo_to_f32(a1[e]);
-        xa[8 + 2 * e + 1] = qp * bf16_hi_to_f32(a1[e]);
+      for (int i = 0; i < 4; ++i) {
+        R[i] = a0[i];
+        R[4 + i] = a1[i];
       }
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        xb[4 * t] = qw * bf16_lo_to_f32(b[t][0]);
-        xb[4 * t + 1] = qw * bf16_hi_to_f32(b[t][0]);
-        xb[4 * t + 2] = qw * bf16_lo_to_f32(b[t][1]);
-        xb[4 * t + 3] = qw * bf16_hi_to_f32(b[t][1]);
-      }
-      const float ca = hig ? 0.5f * W : 0.f, cb = hig ? 0.f : W;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xb0[e] = __builtin_fmaf(xa[e], ca, cb);
     }
-
-    // ---- inter-chunk: O = phi(Q) S (u units), den_inter = phi(Q).z
-    f32x4 O[4];
+    f32x16 O[2] = {splat16(0.f), splat16(0.f)};
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) O[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    float dpart = 0.f;
+    for (int kk = 0; kk < NF / 16; ++kk) {
+      u32x4 bq;
 #pragma unroll
-    for (int ks = 0; ks < 5; ++ks) {
-      float ph[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ph[e] = (ks == 0) ? xa[e] * xb0[e] : xa[e] * xb[(e + ks) & 15];
-      const u32x4 a = {pack_f16x2(ph[0], ph[1]), pack_f16x2(ph[2], ph[3]), pack_f16x2(ph[4], ph[5]),
-                       pack_f16x2(ph[6], ph[7])};
-      if (p.normalize) {
-        const f4 z0 = *reinterpret_cast<const f4*>(&L.Z[32 * ks + 8 * g]);
-        const f4 z1 = *reinterpret_cast<const f4*>(&L.Z[32 * ks + 8 * g + 4]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dpart = __builtin_fmaf(ph[e], z0[e], dpart);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dpart = __builtin_fmaf(ph[4 + e], z1[e], dpart);
+      for (int m = 0; m < 4; ++m) {
+        const Tpl t = tpl(4 * kk + m);
+        u32 v;
+        if (t.t == TL) {
+          v = R[t.a];
+        } else if (t.t == TS) {
+          v = pk_mul_f16(R[t.a], R[t.a]);
+        } else if (t.t == TX) {
+          v = pk_mul_f16(R[t.a], swap16(R[t.a]));
+          if (t.a == 0) v = (v & 0xffffu) | 0x3c000000u;
+        } else {
+          v = pk_mul_f16(R[t.a], t.sw ? swap16(R[t.b]) : R[t.b]);
+        }
+        bq[m] = v;
       }
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const u32x4 b = *reinterpret_cast<const u32x4*>(&L.ST[(16 * nt + r) * STS + 32 * ks + 8 * g]);
-        O[nt] = mfma16_f16(b, a, O[nt]);
+      for (int n = 0; n < 2; ++n) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(&L.ST[(32 * n + r) * STS + 16 * kk + 8 * h]);
+        O[n] = mfma32x32x16_f16(a, bq, O[n]);
       }
     }
 
-    // ---- intra-chunk, d-form: scores S^T (keys x queries) for key tiles kt <= w
-    const u32x4 qb = (g < 2) ? scale_bf16x8(*reinterpret_cast<const u32x4*>(&L.Qs[tl * QKS + 8 * g]), p.qscale)
-                             : (u32x4){0u, 0u, 0u, 0u};
+    // ---- denominator of the earlier tokens: q'^T G q' with q' = [q~ | 1 | 0 ...]; T^T = G Q'^T
+    // on two MFMAs, lane (token r) holds T_i for i = 8 (e >> 2) + 4 h + (e & 3)
+    const u32x4 qb = *reinterpret_cast<const u32x4*>(&L.Q0[(32 * W + r) * QRS + 8 * h]);
+    float dden;
+    {
+      const u32x4 g0 = *reinterpret_cast<const u32x4*>(&L.G16[r * GRS + 8 * h]);
+      const u32x4 g1 = *reinterpret_cast<const u32x4*>(&L.G16[r * GRS + 16 + 8 * h]);
+      const u32x4 one = {h == 0 ? 0x3c00u : 0u, 0u, 0u, 0u};
+      f32x16 T = mfma32x32x16_f16(g0, qb, splat16(0.f));
+      T = mfma32x32x16_f16(g1, one, T);
+      const u32x2 qx = *reinterpret_cast<const u32x2*>(&L.Q0[(32 * W + r) * QRS + 4 * h]);
+      const u32x2 qy = *reinterpret_cast<const u32x2*>(&L.Q0[(32 * W + r) * QRS + 8 + 4 * h]);
+      dden = T[8];   // i = 16 + 4h: the ones component (rows past 16 of G are zero)
+      dden = __builtin_fmaf(T[0], f16_lo_to_f32(qx[0]), dden);
+      dden = __builtin_fmaf(T[1], f16_hi_to_f32(qx[0]), dden);
+      dden = __builtin_fmaf(T[2], f16_lo_to_f32(qx[1]), dden);
+      dden = __builtin_fmaf(T[3], f16_hi_to_f32(qx[1]), dden);
+      dden = __builtin_fmaf(T[4], f16_lo_to_f32(qy[0]), dden);
+      dden = __builtin_fmaf(T[5], f16_hi_to_f32(qy[0]), dden);
+      dden = __builtin_fmaf(T[6], f16_lo_to_f32(qy[1]), dden);
+      dden = __builtin_fmaf(T[7], f16_hi_to_f32(qy[1]), dden);
+    }
+
+    // ---- intra-chunk: key tiles j <= W
     float rs = 0.f;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      if (32 * m > 16 * w + 15) break;
-      float u[2][4];
+    for (int j = 0; j <= W; ++j) {
+      const u32x4 ka = *reinterpret_cast<const u32x4*>(&L.Kr[(32 * j + perm32(r)) * QRS + 8 * h]);
+      const f32x16 sc = mfma32x32x16_f16(ka, qb, splat16(1.0f));
+      u32 pk[8];
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const int kt = 2 * m + h2;
-        if (kt > w) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) u[h2][i] = 0.f;
-          continue;
-        }
-        const u32x4 ka = (g < 2) ? *reinterpret_cast<const u32x4*>(&L.Ks[(16 * kt + r) * QKS + 8 * g])
-                                 : (u32x4){0u, 0u, 0u, 0u};
-        f32x4 b = {inv_c, inv_c, inv_c, inv_c};
-        b = mfma16_bf16(ka, qb, b);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float uu = __builtin_fmaf(b[i], b[i], -inv_c2);
-          const int key = 16 * kt + 4 * g + i;   // chunk-local key of S^T row
-          u[h2][i] = (kt == w && key > tl) ? 0.f : uu;
-        }
+      for (int x = 0; x < 8; ++x) {
+        pk[x] = pack_f16x2(__builtin_fmaf(sc[2 * x], sc[2 * x], 1.0f), __builtin_fmaf(sc[2 * x + 1], sc[2 * x + 1], 1.0f));
+        if (j == W) pk[x] &= dmask[x];
+        rs = dot2_f16(pk[x], kOnes, rs);
       }
-      // S^T C layout: lane (query col r, key rows 4g+i) == A layout of P for keys
-      // {32m + 4g + i, 32m + 16 + 4g + i}
-      const u32x4 pa = {pack_f16x2(u[0][0], u[0][1]), pack_f16x2(u[0][2], u[0][3]), pack_f16x2(u[1][0], u[1][1]),
-                        pack_f16x2(u[1][2], u[1][3])};
-      rs = dot2_f16(pa[0], kOnes, rs);
-      rs = dot2_f16(pa[1], kOnes, rs);
-      rs = dot2_f16(pa[2], kOnes, rs);
-      rs = dot2_f16(pa[3], kOnes, rs);
-      u32 mw[4];
 #pragma unroll
-      for (int c2 = 0; c2 < 4; ++c2) {
-        const int h2 = c2 >> 1, i0 = 2 * (c2 & 1);
-        const int key0 = 32 * m + 16 * h2 + 4 * g + i0;
-        const u32 lo = (key0 <= tl) ? (p.ones_hi & 0xffffu) : 0u;
-        const u32 hi = (key0 + 1 <= tl) ? (p.ones_hi & 0xffff0000u) : 0u;
-        mw[c2] = lo | hi;
-      }
-      const u32x4 mk = {mw[0], mw[1], mw[2], mw[3]};
+      for (int s = 0; s < 2; ++s) {
+        const u32x4 bp = {pk[4 * s], pk[4 * s + 1], pk[4 * s + 2], pk[4 * s + 3]};
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
-        const uint16_t* vp = &L.VT[(16 * nt + r) * VTS + 32 * m + 4 * g];
-        const u32x2 a0 = *reinterpret_cast<const u32x2*>(vp);
-        const u32x2 a1 = *reinterpret_cast<const u32x2*>(vp + 16);
-        const u32x4 vb = {a0[0], a0[1], a1[0], a1[1]};
-        O[nt] = mfma16_f16(vb, pa, O[nt]);
-        O[nt] = mfma16_f16(vb, mk, O[nt]);
-        if (p.ones_lo != 0u) {
-          u32x4 ml;
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            ml[t] = ((mk[t] & 0xffffu) ? (p.ones_lo & 0xffffu) : 0u) |
-                    ((mk[t] & 0xffff0000u) ? (p.ones_lo & 0xffff0000u) : 0u);
-          O[nt] = mfma16_f16(vb, ml, O[nt]);
+        for (int n = 0; n < 2; ++n) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(&L.VT[(32 * n + r) * KRS + 32 * j + 16 * s + 8 * h]);
+          O[n] = mfma32x32x16_f16(a, bp, O[n]);
         }
       }
     }
 
-    // ---- denominator of token tl (A layout, every lane group holds it after the reduction)
-    const float dsum = sum_groups(dpart + rs);   // u units
-    const float den_a = (float)(row0 + tl + 1) + dsum * p.fscale;
-
-    // ---- state update with this chunk (S lives in registers; S^T in LDS is rewritten only
-    // after the next barrier)
-    const float vsc = chunk_vsum_part(L, tid);
-    if ((tid & 3) == 0) L.S0c[tid >> 2] = vsc;
-    if (w < 2)
-      update_slots<3>(L, S, z, w, lane);
-    else
-      update_slots<2>(L, S, z, w, lane);
-
-    // ---- outputs.  O is kept transposed (the 16x16 MFMAs above take V^T / S^T as A), so lane
-    // (token tl, dv rows 16nt + 4g .. +3) holds four consecutive outputs of its own token.
+    // ---- normaliser and outputs.  Lane (token 32W + r, half h) holds dv 32n + 8jj + 4h + i
+    // in O[n][4jj + i]; all values are in units of 2p.
     {
-      const int row = row0 + tl;
-      const float inv = p.normalize ? 1.0f / (den_a + p.eps) : 1.0f;
-      if (row < N) {
+      float x = dden + rs;
+      x += __shfl_xor(x, 32);
+      const float den = (float)row0 + 0.5f * x;
+      // v_rcp_f32 (1 ulp) instead of an IEEE division, and a select, keep this branch-free
+      const float sc = p.normalize ? 0.5f * __builtin_amdgcn_rcpf(den + p.eps) : 0.5f;
+      const int row = row0 + 32 * W + r;
+      if (VEC) {
+        const __amdgpu_buffer_rsrc_t ro =
+            make_rsrc(static_cast<char*>(p.out) + ((size_t)hrow + row0) * dv * esz, (u32)(N - row0) * (u32)dv * (u32)esz);
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int col = 32 * n + 8 * jj + 4 * h;
+            const int voff = col < dv ? ((32 * W + r) * dv + col) * esz : kOffOutOfRange;
+            const float y0 = O[n][4 * jj] * sc, y1 = O[n][4 * jj + 1] * sc;
+            const float y2 = O[n][4 * jj + 2] * sc, y3 = O[n][4 * jj + 3] * sc;
+            if (OUT_F32)
+              buf_store_b128(__builtin_bit_cast(u32x4, (f32x4){y0, y1, y2, y3}), ro, voff);
+            else
+              buf_store_b64((u32x2){pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)}, ro, voff);
+          }
+        }
+      } else if (row < N) {
         const size_t obase = (size_t)(hrow + row) * dv;
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-          const int col = 16 * nt + 4 * g;
-          const f4 s0 = *reinterpret_cast<const f4*>(&L.S0[col]);
-          float y[4];
+        for (int n = 0; n < 2; ++n) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) y[i] = (s0[i] + O[nt][i] * p.fscale) * inv;
-          if (p.vec_out) {
-            if (col < dv) {
-              if (p.out_f32)
-                *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + obase + col) = (f32x4){y[0], y[1], y[2], y[3]};
-              else
-                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + obase + col) =
-                    (u32x2){pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
-            }
-          } else {
+          for (int jj = 0; jj < 4; ++jj) {
+            const int col = 32 * n + 8 * jj + 4 * h;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+              const float y = O[n][4 * jj + i] * sc;
               if (col + i < dv) {
-                if (p.out_f32)
-                  static_cast<float*>(p.out)[obase + col + i] = y[i];
+                if (OUT_F32)
+                  static_cast<float*>(p.out)[obase + col + i] = y;
                 else
-                  static_cast<uint16_t*>(p.out)[obase + col + i] = f32_to_bf16_bits(y[i]);
+                  static_cast<uint16_t*>(p.out)[obase + col + i] = f32_to_bf16_bits(y);
               }
             }
           }
         }
       }
     }
+
+    // ---- state update with this chunk
+    update_blocks<NB>(L.KT, L.VT, S, ra, rb, r, h);
+    if (GRAM) gram_update(L.KT, G, grow, h, 0, 1);
+    stage_convert<true>(st, cv, p.alpha, p.beta);   // next chunk, in registers
+    stage_pin<true>(cv);
+
+    lds_barrier();   // every wave is done with this chunk's tables and the published state
+    if (c + 1 < nch) {
+      stage_write<true>(cv, L.Q0, L.Q1, L.Kr, L.KT, L.VT, lane, W);
+      publish_state<NB>(L, S, OB::first, r, h);
+      if (GRAM) publish_gram(L, G, r, h);
+      lds_barrier();
+    }
   }
 
   // ---- final state of the head (last segment) in the reference feature basis, fp32:
   // state_out[f][0..dv) = sum_u phi_f(k_u) v_u, state_out[f][dv] = sum_u phi_f(k_u)
   if (p.state_out != nullptr && seg == p.P - 1) {
-    __syncthreads();
-    if (tid < DVC) L.S0[tid] += L.S0c[tid];
-    __syncthreads();
-    constexpr int F = 153;
-    float* so = p.state_out + (size_t)bh * F * (dv + 1);
-    if (tid < dv) so[tid] = L.S0[tid];
-    if (tid == 0) so[dv] = (float)N;
+    float* so = p.state_out + (size_t)bh * 153 * (dv + 1);
+    // the Gram matrix in fp32 for the k-sums: G32[i][j], 32 x 33 floats over the S^T table
+    float* G32 = reinterpret_cast<float*>(L.ST);
+    if (GRAM) {
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      if (j >= NS) break;
-      const int s = w + 4 * j;
-      const int dl = slot_delta(s);
-      const float fac = s == 0 ? p.st_lin : (s == 1 ? p.st_diag : p.st_off);
-      // z: row r of the slot (lanes with g == 0 write); delta = 8 rows r and r+8 are one pair
-      float zz = sum_groups(z[j]);
-      const float zpart = __shfl_xor(zz, 8);
-      // S: C layout rows fi = 4g + i; the delta = 8 partner row fi + 8 sits 32 lanes away
+      for (int e = 0; e < 16; ++e) G32[(8 * (e >> 2) + 4 * h + (e & 3)) * 33 + r] = G[e];
+    }
+    lds_barrier();
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt) {
+    for (int b = 0; b < NB; ++b) {
+      const int blk = OB::first + b;
+      // accumulator element e of lane half h is slot 32 blk + 16 (e >> 3) + 8 h + (e & 7)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int fi = 4 * g + i;
-          const float mine = S[j][nt][i];
-          const float other = __shfl_xor(mine, 32);
-          const bool skip = (dl == 8) && fi >= 8;
-          const float val = (dl == 8) ? mine + other : mine;
-          int a = fi, b = (fi + dl) & 15;
-          if (a > b) { const int t2 = a; a = b; b = t2; }
-          const int ref = (s == 0) ? 1 + fi : (s == 1 ? 17 + fi : 33 + a * (31 - a) / 2 + (b - a - 1));
-          const int col = 16 * nt + r;
-          if (!skip && col < dv) so[(size_t)ref * (dv + 1) + col] = val * fac;
+      for (int e = 0; e < 16; ++e) {
+        const int f = 32 * blk + 16 * (e >> 3) + 8 * h + (e & 7);
+        const RefFeat rf = ref_feature(f);
+        if (rf.ref < 0) continue;
+        const float fac = p.st_fac[rf.fac];
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+          const int col = 32 * n + r;
+          if (col < dv) so[(size_t)rf.ref * (dv + 1) + col] = S[b][n][e] * fac;
         }
       }
-      if (g == 0 && !((dl == 8) && r >= 8)) {
-        int a = r, b = (r + dl) & 15;
-        if (a > b) { const int t2 = a; a = b; b = t2; }
-        const int ref = (s == 0) ? 1 + r : (s == 1 ? 17 + r : 33 + a * (31 - a) / 2 + (b - a - 1));
-        so[(size_t)ref * (dv + 1) + dv] = ((dl == 8) ? zz + zpart : zz) * fac;
+      // k-sums of the slots of rows r of the update tile (lane half 0)
+      const int f = block_slot(blk, r);
+      const RefFeat rf = ref_feature(f);
+      if (h == 0 && rf.ref >= 0) {
+        const KRows kr = krows(f);
+        int da, db;
+        float fa, fb;
+        kt_row_dim(kr.a, da, fa);
+        kt_row_dim(kr.b, db, fb);
+        const float z = fa * fb * G32[da * 33 + db];
+        so[(size_t)rf.ref * (dv + 1) + dv] = rf.ref == 0 ? (float)N : z * p.st_fac[rf.fac];
       }
     }
   }
 }
 
-// Segment split: enough (head, segment) work-groups to fill the GPU twice over.
+template <bool VEC, bool OUT_F32>
+__global__ __launch_bounds__(64 * NWAVE_OUT, 2) void chunked_output_kernel(const ChunkParams p) {
+  __shared__ __attribute__((aligned(16))) OutLds L;
+  int bh, seg;
+  map_segment(blockIdx.x, p.BH, p.P, bh, seg);
+  switch (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) {
+    case 0: output_wave<0, VEC, OUT_F32>(L, p, bh, seg); break;
+    case 1: output_wave<1, VEC, OUT_F32>(L, p, bh, seg); break;
+    case 2: output_wave<2, VEC, OUT_F32>(L, p, bh, seg); break;
+    default: output_wave<3, VEC, OUT_F32>(L, p, bh, seg); break;
+  }
+}
+
+// Segment split: enough (head, segment) work-groups to fill the GPU twice over, at most
+// MAX_SEG segments per head.
 void segment_split(int BH, int N, int& P, int& seg_chunks) {
   const int nchunks = (N + CH - 1) / CH;
   P = (512 + BH - 1) / BH;
+  if (P > MAX_SEG) P = MAX_SEG;
   if (P > nchunks) P = nchunks;
   if (P < 1) P = 1;
   seg_chunks = (nchunks + P - 1) / P;
@@ -701,13 +861,14 @@ size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk) {
   if (d != 16 || dv > 64 || chunk < 1) return (size_t)-1;
   int P, seg_chunks;
   segment_split(BH, N, P, seg_chunks);
-  const size_t per = (size_t)DVC * NF * 2 + (size_t)NF * 4 + (size_t)DVC * 4;
+  const size_t per = (size_t)64 * NF * 2 + (size_t)1024 * 4;
   return (size_t)BH * P * per + 256;
 }
 
 int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
   if (a.d != 16 || a.dv > 64) return LA_ERR_UNSUPPORTED_DIM;
   if (a.in_f32) return LA_ERR_BAD_DTYPE;
+  if ((reinterpret_cast<uintptr_t>(a.q) & 7) || (reinterpret_cast<uintptr_t>(a.k) & 7)) return LA_ERR_BAD_ALIGNMENT;
   ChunkParams p{};
   p.q = static_cast<const uint16_t*>(a.q);
   p.k = static_cast<const uint16_t*>(a.k);
@@ -721,64 +882,51 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
   segment_split(a.BH, a.N, P, seg_chunks);
   p.P = P;
   p.seg_chunks = seg_chunks;
-  const size_t sS = (size_t)a.BH * P * DVC * NF * 2, sZ = (size_t)a.BH * P * NF * 4;
+  const size_t sS = (size_t)a.BH * P * 64 * NF * 2;
   char* ws = static_cast<char*>(a.workspace);
   p.wsS = reinterpret_cast<uint16_t*>(ws);
-  p.wsZ = reinterpret_cast<float*>(ws + sS);
-  p.wsV = reinterpret_cast<float*>(ws + sS + sZ);
-  // intra d-form constants (same as the parallel kernel)
-  const double ic = 1.0 / (double)a.scale;
-  const int k = (int)lround(0.5 * log2(2.0 * ic * ic) - 0.25);
-  const double qs = ldexp(1.0, -k);
-  const float icf = (float)(ic * qs);
-  p.qscale = (float)qs;
-  p.inv_c = icf;
-  p.inv_c2 = (float)((double)icf * (double)icf);
-  const double w = 2.0 * (double)icf * (double)icf;
-  p.W = (float)w;
-  p.fscale = (float)(1.0 / w);
-  const _Float16 whi = (_Float16)w;
-  const _Float16 wlo = (_Float16)(w - (double)whi);
-  const u32 hb = __builtin_bit_cast(uint16_t, whi), lb = __builtin_bit_cast(uint16_t, wlo);
-  p.ones_hi = hb | (hb << 16);
-  p.ones_lo = ((double)wlo == 0.0) ? 0u : (lb | (lb << 16));
-  // feature scaling: q~ = sqrt(c) 2^(sigma/2) q, k~ = sqrt(c) 2^(-sigma/2) k
+  p.wsG = reinterpret_cast<float*>(ws + sS);
+  // q~ = alpha q, k~ = beta k with alpha beta = scale; sigma moves magnitude from the state
+  // (sums over up to N tokens) to the q side so that it stays well inside the fp16 range.
   int sigma = 0;
   while ((1 << (sigma + 10)) < a.N && sigma < 12) sigma += 2;
   const double rc = sqrt((double)a.scale);
-  p.qphi = (float)(rc * ldexp(1.0, sigma / 2));
-  p.kphi = (float)(rc * ldexp(1.0, -sigma / 2));
-  p.st_lin = (float)ldexp(1.0, sigma / 2);
-  p.st_diag = (float)(ldexp(1.0, sigma) / sqrt(2.0));
-  p.st_off = (float)ldexp(1.0, sigma);
+  p.alpha = (float)(rc * ldexp(1.0, sigma / 2));
+  p.beta = (float)(rc * ldexp(1.0, -sigma / 2));
+  // internal k side -> reference features: constant 2, linear 2 k~, square k~^2, pair 2 k~ k~
+  p.st_fac[0] = 0.5f;
+  p.st_fac[1] = (float)(ldexp(1.0, sigma / 2) * 0.5);
+  p.st_fac[2] = (float)(ldexp(1.0, sigma) / sqrt(2.0));
+  p.st_fac[3] = (float)(ldexp(1.0, sigma) * 0.5);
   p.eps = a.eps;
   p.normalize = a.normalize ? 1 : 0;
   p.out_f32 = a.out_f32 ? 1 : 0;
-  const bool vec = (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
-                   ((reinterpret_cast<uintptr_t>(a.k) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 7) == 0);
-  p.vec = vec;
+  const bool vec_v = (a.dv % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 15) == 0);
   p.vec_out = (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0);
-  const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
   if (P > 1) {
     const dim3 grid((unsigned)(a.BH * (P - 1)));
-    if (vec)
-      hipLaunchKernelGGL(chunked_segment_kernel<true>, grid, dim3(256), 0, stream, p);
+    if (vec_v)
+      hipLaunchKernelGGL(chunked_segment_kernel<true>, grid, dim3(64 * NWAVE_SEG), 0, stream, p);
     else
-      hipLaunchKernelGGL(chunked_segment_kernel<false>, grid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL(chunked_segment_kernel<false>, grid, dim3(64 * NWAVE_SEG), 0, stream, p);
     int e = (int)hipGetLastError();
     if (e != 0) return e;
-    const dim3 pgrid((unsigned)((DVC * NF + NF + DVC + 255) / 256), (unsigned)a.BH);
+    const dim3 pgrid((unsigned)((64 * NF / 8 + 1024 / 4 + 255) / 256), (unsigned)a.BH);
     hipLaunchKernelGGL(chunked_prefix_kernel, pgrid, dim3(256), 0, stream, p);
     e = (int)hipGetLastError();
     if (e != 0) return e;
   }
   const dim3 grid((unsigned)(a.BH * P));
-  if (vec && unit)
-    hipLaunchKernelGGL((chunked_output_kernel<true, true>), grid, dim3(256), 0, stream, p);
+  const dim3 block(64 * NWAVE_OUT);
+  const bool vec = vec_v && p.vec_out;
+  if (vec && a.out_f32)
+    hipLaunchKernelGGL((chunked_output_kernel<true, true>), grid, block, 0, stream, p);
   else if (vec)
-    hipLaunchKernelGGL((chunked_output_kernel<true, false>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((chunked_output_kernel<true, false>), grid, block, 0, stream, p);
+  else if (a.out_f32)
+    hipLaunchKernelGGL((chunked_output_kernel<false, true>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((chunked_output_kernel<false, false>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((chunked_output_kernel<false, false>), grid, block, 0, stream, p);
   return (int)hipGetLastError();
 }
 

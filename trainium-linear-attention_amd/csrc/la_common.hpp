@@ -146,4 +146,30 @@ __device__ __forceinline__ u32 lds_addr(const T* p) {
   return (u32)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
+// ---- raw buffer loads / stores
+//
+// A raw buffer resource over [base, base + bytes) (dword 3 as for buffer_rsrc above): accesses at
+// offsets >= bytes read as zero and are dropped on store, which takes the place of per-lane
+// bounds checks.  base and bytes must be wave-uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, u32 bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+// An offset that is out of range for every resource built by make_rsrc (bytes < 2^31).
+constexpr int kOffOutOfRange = 0x7ffffff0;
+
+__device__ __forceinline__ u32x2 buf_load_b64(__amdgpu_buffer_rsrc_t r, int voff) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, 0, 0));
+}
+__device__ __forceinline__ u32x4 buf_load_b128(__amdgpu_buffer_rsrc_t r, int voff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+__device__ __forceinline__ void buf_store_b64(u32x2 x, __amdgpu_buffer_rsrc_t r, int voff) {
+  typedef __attribute__((__vector_size__(2 * sizeof(u32)))) u32 v2;
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2, x), r, voff, 0, 0);
+}
+__device__ __forceinline__ void buf_store_b128(u32x4 x, __amdgpu_buffer_rsrc_t r, int voff) {
+  typedef __attribute__((__vector_size__(4 * sizeof(u32)))) u32 v4;
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4, x), r, voff, 0, 0);
+}
+
 }  // namespace la
