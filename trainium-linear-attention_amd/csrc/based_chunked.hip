@@ -15,10 +15,10 @@
 //     feature slots (10 K-steps of 16) holding the 153 distinct features of the symmetric
 //     Taylor map: the constant, q~_i, q~_i^2 and q~_i q~_j (i < j).  The q side of a K-step is
 //     four packed-fp16 products of q~'s eight register pairs R_x = (q~_2x, q~_2x+1); the two
-//     lane halves of the MFMA operand hold q~ rotated by one register, so one v_pk_mul_f16
-//     yields two features for each half ("templates" below).  All coefficients live on the k
-//     side, which multiplies two rows of an LDS table [k~ | 2 k~ | 1 | 0 | 2] (K^T, token pairs
-//     packed), again one v_pk_mul_f16 per two products.
+//     lane halves of the MFMA operand hold q~ rotated by two registers, so one v_pk_mul_f16
+//     yields two features for each half ("templates" below).  The k side multiplies two rows of
+//     an LDS table [k~ | 1 | 0 | 2] (K^T, token pairs packed), again one v_pk_mul_f16 per two
+//     products; the factor 2 of the linear and mixed terms is on the q side.
 //   * The state S (160 x dv, fp32 MFMA accumulators) stays in registers across chunks,
 //     partitioned over the waves by blocks of 32 features; every chunk it is published to LDS
 //     as fp16 S^T for the inter-chunk product phi(Q) S of all waves.
@@ -47,8 +47,8 @@ constexpr int NF = 160;         // feature slots
 constexpr int QRS = 24;         // row stride (halves) of the q~ / k~ row tables: 48 B
 constexpr int KRS = 136;        // row stride (halves) of the K^T and V^T tables: 272 B
 constexpr int STS = 168;        // row stride (halves) of S^T: 336 B
-constexpr int KT_ROWS = 36;
-constexpr int R_ONES = 32, R_ZA = 33, R_ZB = 34, R_TWOS = 35;   // constant rows of K^T
+constexpr int KT_ROWS = 20;
+constexpr int R_ONES = 16, R_ZA = 17, R_ZB = 18, R_TWOS = 19;   // constant rows of K^T
 constexpr int NWAVE_OUT = 4;
 constexpr int NWAVE_SEG = 5;
 constexpr int MAX_SEG = 32;
@@ -56,23 +56,24 @@ constexpr int MAX_SEG = 32;
 // ---- feature templates
 //
 // Slot f = 16 kk + 8 h + 2 m + e: K-step kk, lane half h, packed register m, half e.  The q side
-// of (kk, m) is template tpl(4 kk + m) applied to the register pairs R'_x = R_{(x + h) mod 8}:
-//   L a     : R'_a                        (q~_i)
+// of (kk, m) is template tpl(4 kk + m) applied to the register pairs R'_x = R_{(x + 2h) mod 8}
+// (and R2' = 2 R'):
+//   L a     : R2'_a                       (2 q~_i)
 //   S a     : R'_a * R'_a                 (q~_i^2)
-//   X a     : R'_a * swap(R'_a)           (q~_2x q~_2x+1 in the low half; the high half
+//   X a     : R2'_a * swap(R'_a)          (2 q~_2x q~_2x+1 in the low half; the high half
 //                                          duplicates it and is unused, except for a = 0 where
 //                                          it is replaced by 1: the constant feature)
-//   P a b s : R'_a * (s ? swap(R'_b) : R'_b)
-// The rotation by h makes every template cover two disjoint sets of registers, so the 40
+//   P a b s : R2'_a * (s ? swap(R'_b) : R'_b)
+// The rotation by 2h makes every template cover two disjoint sets of registers, so the 40
 // templates hold each of the 153 features exactly once.  Templates of one K-step share the
-// type and use a = 0, 2, 4, 6, which keeps the k-side row reads of a K-step on distinct LDS
+// type and use a = 0, 1, 4, 5, which keeps the k-side row reads of a K-step on distinct LDS
 // banks.
 enum { TL = 0, TS = 1, TX = 2, TP = 3 };
 struct Tpl {
   int t, a, b, sw;
 };
 __host__ __device__ constexpr Tpl tpl(int i) {
-  const int kk = i >> 2, m = i & 3, a = 2 * m;
+  const int kk = i >> 2, m = i & 3, a = (m & 1) + 4 * (m >> 1);   // 0, 1, 4, 5
   if (kk == 0) return Tpl{TL, a, 0, 0};
   if (kk == 1) return Tpl{TS, a, 0, 0};
   if (kk == 2) return Tpl{TX, a, 0, 0};
@@ -87,26 +88,26 @@ struct KRows {
 __host__ __device__ constexpr KRows krows(int f) {
   const int kk = f >> 4, h = (f >> 3) & 1, m = (f >> 1) & 3, e = f & 1;
   const Tpl t = tpl(4 * kk + m);
-  const int x = (t.a + h) & 7, y = (t.b + h) & 7;
-  if (t.t == TL) return KRows{16 + 2 * x + e, R_ONES};
+  const int x = (t.a + 2 * h) & 7, y = (t.b + 2 * h) & 7;
+  if (t.t == TL) return KRows{2 * x + e, R_ONES};
   if (t.t == TS) return KRows{2 * x + e, 2 * x + e};
   if (t.t == TX) {
-    if (e == 0) return KRows{2 * x, 16 + 2 * x + 1};
+    if (e == 0) return KRows{2 * x, 2 * x + 1};
     return (t.a == 0 && h == 0) ? KRows{R_TWOS, R_ONES} : KRows{R_ZA, R_ZB};
   }
-  return KRows{2 * x + e, 16 + (t.sw ? 2 * y + 1 - e : 2 * y + e)};
+  return KRows{2 * x + e, t.sw ? 2 * y + 1 - e : 2 * y + e};
 }
 
 // Reference feature (benchmarks/chunked_attention_benchmark.py:34-53 order: 1, x_i, x_i^2,
 // x_i x_j for i < j row-major) of slot f, and the factor from the internal k side to it as
-// an index into {1/2, 2^(sigma/2)/2, 2^sigma/sqrt 2, 2^sigma/2}; ref = -1 for unused slots.
+// an index into {1/2, 2^(sigma/2), 2^sigma/sqrt 2, 2^sigma}; ref = -1 for unused slots.
 struct RefFeat {
   int ref, fac;
 };
 __host__ __device__ constexpr RefFeat ref_feature(int f) {
   const int kk = f >> 4, h = (f >> 3) & 1, m = (f >> 1) & 3, e = f & 1;
   const Tpl t = tpl(4 * kk + m);
-  const int x = (t.a + h) & 7, y = (t.b + h) & 7;
+  const int x = (t.a + 2 * h) & 7, y = (t.b + 2 * h) & 7;
   int i = 0, j = 0;
   if (t.t == TL) return RefFeat{1 + 2 * x + e, 1};
   if (t.t == TS) return RefFeat{17 + 2 * x + e, 2};
@@ -160,11 +161,10 @@ constexpr int GRS = 40;   // row stride (halves) of the fp16 Gram matrix in LDS:
 
 // LDS image of one chunk and of the published state.
 struct OutLds {
-  uint16_t Q0[CH * QRS];        // q~ rows (fp16)
-  uint16_t Q1[CH * QRS];        // q~ rows rotated left by two elements
+  uint16_t Q0[CH * QRS];        // q~ rows (fp16): q~_0 .. q~_15, q~_0 .. q~_3
   uint16_t Kr[CH * QRS];        // k~ rows
-  uint16_t KT[KT_ROWS * KRS];   // k~^T, (2 k~)^T, constant rows
-  uint16_t VT[64 * KRS];        // V^T
+  uint16_t KT[KT_ROWS * KRS];   // k~^T, constant rows
+  uint16_t VT[64 * KRS];        // V^T, 16-byte units swizzled by row (vt_off)
   uint16_t ST[64 * STS];        // S^T (feature slots)
   uint16_t G16[32 * GRS];       // Gram matrix [k~ | 1]^T [k~ | 1] of earlier tokens, (16,16) zeroed
 };
@@ -185,6 +185,11 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ u32 swap16(u32 x) { return __builtin_amdgcn_alignbit(x, x, 16); }
 
+// Half index of the 16-byte unit u (tokens 8u .. 8u + 7) of V^T row c.  The XOR spreads the
+// staging stores (8 rows 8 apart per instruction) over all banks; MFMA operand reads (16
+// consecutive rows, one unit) stay conflict-free.
+__device__ __forceinline__ int vt_off(int c, int u) { return c * KRS + 8 * (u ^ (2 * (c >> 4))); }
+
 // Constant rows of the K^T table (written once per kernel).
 __device__ __forceinline__ void init_kt_constants(uint16_t* KT, int tid, int nthreads) {
   for (int i = tid; i < 4 * (CH / 2); i += nthreads) {
@@ -199,97 +204,100 @@ __device__ __forceinline__ int gram_row(int rho) { return rho < 16 ? rho : (rho 
 
 // ---- staging: global -> registers -> (convert) -> LDS
 //
-// Wave wv (0..3) stages q, k dims 4 wv .. +3 and v dims 16 wv .. +15; lane l the token pair
-// 2l, 2l + 1 of the chunk, so that every LDS store instruction writes consecutive dwords of one
-// table row.
+// Every load instruction of a wave reads whole 128-byte lines.  Wave wv (0..3), lane l:
+//   q, k: token 32 wv + l/2, dims 8 (l % 2) .. +7 (16 B; a wave reads 1 KB contiguous);
+//   v:    tokens 32 wv + 16 pp + 2 (l/8) + {0, 1} (pp = 0, 1), dims 8 (l % 8) .. +7, i.e. eight
+//         full rows per instruction.
+// K^T needs token pairs: lanes l and l ^ 2 hold tokens 2i, 2i + 1 and swap half their dims.
 struct StageRegs {
-  u32x2 q[2], k[2];
-  u32x4 v[2][2];
+  u32x4 q, k;
+  u32x4 v[2][2];   // [pp][token of the pair]
 };
 
+// row0 < N; with valid false every load reads zero without touching memory (empty resource),
+// which lets a loop issue its look-ahead load unconditionally.
 template <bool VEC_V, bool WITH_Q>
 __device__ __forceinline__ void stage_load(StageRegs& s, const ChunkParams& p, const uint16_t* qh,
-                                           const uint16_t* kh, const uint16_t* vh, int row0, int l, int wv) {
+                                           const uint16_t* kh, const uint16_t* vh, int row0, int l, int wv,
+                                           bool valid = true) {
   const int N = p.N, dv = p.dv;
-  const u32 rem = (u32)(N - row0);   // > 0
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(kh + (size_t)row0 * 16, rem * 32u);
-  __amdgpu_buffer_rsrc_t rq = rk;
-  if (WITH_Q) rq = make_rsrc(qh + (size_t)row0 * 16, rem * 32u);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int voff = (2 * l + j) * 32 + 8 * wv;
-    if (WITH_Q) s.q[j] = buf_load_b64(rq, voff);
-    s.k[j] = buf_load_b64(rk, voff);
+  const u32 rem = valid ? (u32)(N - row0) : 0u;
+  {
+    const int voff = (32 * wv + (l >> 1)) * 32 + 16 * (l & 1);
+    s.k = buf_load_b128(make_rsrc(kh + (size_t)row0 * 16, rem * 32u), voff);
+    if (WITH_Q) s.q = buf_load_b128(make_rsrc(qh + (size_t)row0 * 16, rem * 32u), voff);
   }
+  const int col = 8 * (l & 7);
   if (VEC_V) {
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vh + (size_t)row0 * dv, rem * (u32)dv * 2u);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
-      for (int hv = 0; hv < 2; ++hv) {
-        const int col = 16 * wv + 8 * hv;
-        const int voff = col < dv ? ((2 * l + j) * dv + col) * 2 : kOffOutOfRange;
-        s.v[j][hv] = buf_load_b128(rv, voff);
+      for (int j = 0; j < 2; ++j) {
+        const int t = 32 * wv + 16 * pp + 2 * (l >> 3) + j;
+        s.v[pp][j] = buf_load_b128(rv, col < dv ? (t * dv + col) * 2 : kOffOutOfRange);
       }
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int row = row0 + 2 * l + j;
+    for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
-      for (int hv = 0; hv < 2; ++hv) {
-        const int col = 16 * wv + 8 * hv;
+      for (int j = 0; j < 2; ++j) {
+        const int row = row0 + 32 * wv + 16 * pp + 2 * (l >> 3) + j;
         uint16_t e[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) e[i] = (row < N && col + i < dv) ? vh[(size_t)row * dv + col + i] : (uint16_t)0;
-        s.v[j][hv] = (u32x4){e[0] | ((u32)e[1] << 16), e[2] | ((u32)e[3] << 16), e[4] | ((u32)e[5] << 16),
+        for (int i = 0; i < 8; ++i)
+          e[i] = (valid && row < N && col + i < dv) ? vh[(size_t)row * dv + col + i] : (uint16_t)0;
+        s.v[pp][j] = (u32x4){e[0] | ((u32)e[1] << 16), e[2] | ((u32)e[3] << 16), e[4] | ((u32)e[5] << 16),
                              e[6] | ((u32)e[7] << 16)};
       }
     }
   }
 }
 
-// Converted staging values of one thread: fp16 q~ / k~ row pieces, k~ and 2 k~ token pairs of
-// dims 4 wv + i, V^T token pairs of dims 16 wv + 2 i (+1).
+// Converted staging values of one thread: q~ / k~ row pieces (dims 8 (l % 2) .. +7), k~ token
+// pairs of four dims, V^T token pairs of dims 8 (l % 8) + e for the two token pairs pp.
 struct StageConv {
-  u32 q[2][2], kr[2][2];
-  u32 kt[4], kt2[4];
-  u32 vt[16];
+  u32x4 q, kr;
+  u32 kt[4];
+  u32 vt[2][8];
 };
 
+__device__ __forceinline__ u32 swap_quad_pairs(u32 x) {
+  // lanes l and l ^ 2 exchange (DPP quad_perm [2, 3, 0, 1])
+  return (u32)__builtin_amdgcn_mov_dpp((int)x, 0x4e, 0xf, 0xf, false);
+}
+
 template <bool WITH_Q>
-__device__ __forceinline__ void stage_convert(const StageRegs& s, StageConv& o, float alpha, float beta) {
+__device__ __forceinline__ void stage_convert(const StageRegs& s, StageConv& o, float alpha, float beta, int l) {
   if (WITH_Q) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      o.q[j][0] = pack_f16x2(alpha * bf16_lo_to_f32(s.q[j][0]), alpha * bf16_hi_to_f32(s.q[j][0]));
-      o.q[j][1] = pack_f16x2(alpha * bf16_lo_to_f32(s.q[j][1]), alpha * bf16_hi_to_f32(s.q[j][1]));
-    }
+    for (int i = 0; i < 4; ++i)
+      o.q[i] = pack_f16x2(alpha * bf16_lo_to_f32(s.q[i]), alpha * bf16_hi_to_f32(s.q[i]));
   }
-  float kf[2][4];
+  // K^T pairs: the even-token lane of a pair keeps dims +0..3, the odd-token lane dims +4..7
+  const bool odd = (l >> 1) & 1;
+  const u32 send0 = odd ? s.k[0] : s.k[2], send1 = odd ? s.k[1] : s.k[3];
+  const u32 got0 = swap_quad_pairs(send0), got1 = swap_quad_pairs(send1);
+  const u32 own0 = odd ? s.k[2] : s.k[0], own1 = odd ? s.k[3] : s.k[1];
+  const u32 ev0 = odd ? got0 : own0, ev1 = odd ? got1 : own1;   // even token, 4 dims (bf16)
+  const u32 od0 = odd ? own0 : got0, od1 = odd ? own1 : got1;   // odd token
+  o.kt[0] = pack_f16x2(beta * bf16_lo_to_f32(ev0), beta * bf16_lo_to_f32(od0));
+  o.kt[1] = pack_f16x2(beta * bf16_hi_to_f32(ev0), beta * bf16_hi_to_f32(od0));
+  o.kt[2] = pack_f16x2(beta * bf16_lo_to_f32(ev1), beta * bf16_lo_to_f32(od1));
+  o.kt[3] = pack_f16x2(beta * bf16_hi_to_f32(ev1), beta * bf16_hi_to_f32(od1));
+  if (WITH_Q) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    kf[j][0] = beta * bf16_lo_to_f32(s.k[j][0]);
-    kf[j][1] = beta * bf16_hi_to_f32(s.k[j][0]);
-    kf[j][2] = beta * bf16_lo_to_f32(s.k[j][1]);
-    kf[j][3] = beta * bf16_hi_to_f32(s.k[j][1]);
-    if (WITH_Q) {
-      o.kr[j][0] = pack_f16x2(kf[j][0], kf[j][1]);
-      o.kr[j][1] = pack_f16x2(kf[j][2], kf[j][3]);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o.kt[i] = pack_f16x2(kf[0][i], kf[1][i]);   // (token 2l, token 2l+1) of dim 4wv+i
-    o.kt2[i] = pk_mul_f16(o.kt[i], 0x40004000u);
+    for (int i = 0; i < 4; ++i)
+      o.kr[i] = pack_f16x2(beta * bf16_lo_to_f32(s.k[i]), beta * bf16_hi_to_f32(s.k[i]));
   }
 #pragma unroll
-  for (int hv = 0; hv < 2; ++hv) {
+  for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const u32 a = s.v[0][hv][w], b = s.v[1][hv][w];
-      o.vt[2 * (4 * hv + w)] = pack_f16x2(bf16_lo_to_f32(a), bf16_lo_to_f32(b));
-      o.vt[2 * (4 * hv + w) + 1] = pack_f16x2(bf16_hi_to_f32(a), bf16_hi_to_f32(b));
+      const u32 a = s.v[pp][0][w], b = s.v[pp][1][w];
+      o.vt[pp][2 * w] = pack_f16x2(bf16_lo_to_f32(a), bf16_lo_to_f32(b));
+      o.vt[pp][2 * w + 1] = pack_f16x2(bf16_hi_to_f32(a), bf16_hi_to_f32(b));
     }
   }
 }
@@ -299,40 +307,39 @@ __device__ __forceinline__ void stage_convert(const StageRegs& s, StageConv& o, 
 template <bool WITH_Q>
 __device__ __forceinline__ void stage_pin(StageConv& o) {
   if (WITH_Q) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(o.q[j][0]), "+v"(o.q[j][1]), "+v"(o.kr[j][0]), "+v"(o.kr[j][1]));
+    asm volatile("" : "+v"(o.q[0]), "+v"(o.q[1]), "+v"(o.q[2]), "+v"(o.q[3]));
+    asm volatile("" : "+v"(o.kr[0]), "+v"(o.kr[1]), "+v"(o.kr[2]), "+v"(o.kr[3]));
   }
+  asm volatile("" : "+v"(o.kt[0]), "+v"(o.kt[1]), "+v"(o.kt[2]), "+v"(o.kt[3]));
 #pragma unroll
-  for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(o.kt[i]), "+v"(o.kt2[i]));
+  for (int pp = 0; pp < 2; ++pp)
 #pragma unroll
-  for (int i = 0; i < 16; i += 4) asm volatile("" : "+v"(o.vt[i]), "+v"(o.vt[i + 1]), "+v"(o.vt[i + 2]), "+v"(o.vt[i + 3]));
+    for (int i = 0; i < 8; i += 4) asm volatile("" : "+v"(o.vt[pp][i]), "+v"(o.vt[pp][i + 1]), "+v"(o.vt[pp][i + 2]), "+v"(o.vt[pp][i + 3]));
 }
 
 template <bool WITH_Q>
-__device__ __forceinline__ void stage_write(const StageConv& o, uint16_t* Q0, uint16_t* Q1, uint16_t* Kr,
-                                            uint16_t* KT, uint16_t* VT, int l, int wv) {
-  const int dq = wv;
+__device__ __forceinline__ void stage_write(const StageConv& o, uint16_t* Q0, uint16_t* Kr, uint16_t* KT, uint16_t* VT,
+                                            int l, int wv) {
   if (WITH_Q) {
+    const int t = 32 * wv + (l >> 1), c = 8 * (l & 1);
+    *reinterpret_cast<u32x4*>(&Q0[t * QRS + c]) = o.q;
+    if ((l & 1) == 0) *reinterpret_cast<u32x2*>(&Q0[t * QRS + 16]) = (u32x2){o.q[0], o.q[1]};   // q~_0..3 again
+    *reinterpret_cast<u32x4*>(&Kr[t * QRS + c]) = o.kr;
+  }
+  {
+    const int tp = 16 * wv + (l >> 2);                       // token pair
+    const int d0 = 8 * (l & 1) + 4 * ((l >> 1) & 1);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int tok = 2 * l + j;
-      *reinterpret_cast<u32x2*>(&Q0[tok * QRS + 4 * dq]) = (u32x2){o.q[j][0], o.q[j][1]};
-      // rotated copy: element i of Q1 is element (i + 2) mod 16 of q~
-      *reinterpret_cast<u32*>(&Q1[tok * QRS + ((4 * dq + 14) & 15)]) = o.q[j][0];
-      *reinterpret_cast<u32*>(&Q1[tok * QRS + 4 * dq]) = o.q[j][1];
-      *reinterpret_cast<u32x2*>(&Kr[tok * QRS + 4 * dq]) = (u32x2){o.kr[j][0], o.kr[j][1]};
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32*>(&KT[(d0 + i) * KRS + 2 * tp]) = o.kt[i];
+  }
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp) {
+    const int tp = 16 * wv + 8 * pp + (l >> 3);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = 8 * (l & 7) + e;
+      *reinterpret_cast<u32*>(&VT[vt_off(d, tp >> 2) + 2 * (tp & 3)]) = o.vt[pp][e];
     }
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    *reinterpret_cast<u32*>(&KT[(4 * dq + i) * KRS + 2 * l]) = o.kt[i];
-    *reinterpret_cast<u32*>(&KT[(16 + 4 * dq + i) * KRS + 2 * l]) = o.kt2[i];
-  }
-  // V^T: row c = 16 dq + 2 i (+1), token pair l
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    *reinterpret_cast<u32*>(&VT[(16 * dq + 2 * i) * KRS + 2 * l]) = o.vt[2 * i];
-    *reinterpret_cast<u32*>(&VT[(16 * dq + 2 * i + 1) * KRS + 2 * l]) = o.vt[2 * i + 1];
   }
 }
 
@@ -347,7 +354,7 @@ __device__ __forceinline__ void update_blocks(const uint16_t* KT, const uint16_t
   for (int s = 0; s < CH / 16; ++s) {
     u32x4 bv[2];
 #pragma unroll
-    for (int n = 0; n < 2; ++n) bv[n] = *reinterpret_cast<const u32x4*>(&VT[(32 * n + r) * KRS + 16 * s + 8 * h]);
+    for (int n = 0; n < 2; ++n) bv[n] = *reinterpret_cast<const u32x4*>(&VT[vt_off(32 * n + r, 2 * s + h)]);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const u32x4 x = *reinterpret_cast<const u32x4*>(&KT[ra[b] + 16 * s + 8 * h]);
@@ -375,7 +382,6 @@ __device__ __forceinline__ int block_slot(int b, int r) { return 32 * b + perm32
 // Gram coordinate and factor of a K^T row: z_f = fa fb G[da][db] for slot rows (a, b).
 __device__ __forceinline__ void kt_row_dim(int row, int& d, float& f) {
   if (row < 16) { d = row; f = 1.f; }
-  else if (row < 32) { d = row - 16; f = 2.f; }
   else if (row == R_ONES) { d = 16; f = 1.f; }
   else if (row == R_TWOS) { d = 16; f = 2.f; }
   else { d = 0; f = 0.f; }
@@ -384,18 +390,29 @@ __device__ __forceinline__ void kt_row_dim(int row, int& d, float& f) {
 // -------------------------------------------------------------------------------------------
 // Kernel 1: state increment of every segment but the last.  Work-group (head, segment); wave w
 // owns feature block w (all dv) and K-steps w, w + 5 of the Gram matrix; waves 0..3 stage.
+// A work-group runs two segments side by side (waves 0..4 and 5..9, each with its own LDS
+// tables; barriers are shared): two 5-wave work-groups per CU do not get co-scheduled, one
+// 10-wave work-group spreads 3 / 3 / 2 / 2 waves over the SIMDs.
+constexpr int SEG_PER_WG = 2;
 template <bool VEC_V>
-__global__ __launch_bounds__(64 * NWAVE_SEG) void chunked_segment_kernel(const ChunkParams p) {
-  __shared__ __attribute__((aligned(16))) SegLds L;
-  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+__global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_kernel(const ChunkParams p) {
+  __shared__ __attribute__((aligned(16))) SegLds Ls[SEG_PER_WG];
+  const int wall = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = wall / NWAVE_SEG, w = wall - sub * NWAVE_SEG;
+  const int tid = threadIdx.x - sub * 64 * NWAVE_SEG, lane = tid & 63;
   const int r = lane & 31, h = lane >> 5;
+  SegLds& L = Ls[sub];
+  const int nseg_total = p.BH * (p.P - 1);
+  int gseg = blockIdx.x * SEG_PER_WG + sub;
+  const bool active = gseg < nseg_total;   // the last work-group may have an idle half
+  if (!active) gseg = nseg_total - 1;
   int bh, seg;
-  map_segment(blockIdx.x, p.BH, p.P - 1, bh, seg);
+  map_segment(gseg, p.BH, p.P - 1, bh, seg);
   const size_t hrow = (size_t)bh * p.N;
   const uint16_t* kh = p.k + hrow * 16;
   const uint16_t* vh = p.v + hrow * p.dv;
   const int c0 = seg * p.seg_chunks, nch = p.seg_chunks;
-  const bool stager = w < 4;
+  const bool stager = w < 4 && active;
 
   const KRows kr = krows(block_slot(w, r));
   const int ra[1] = {kr.a * KRS}, rb[1] = {kr.b * KRS};
@@ -405,32 +422,41 @@ __global__ __launch_bounds__(64 * NWAVE_SEG) void chunked_segment_kernel(const C
 
   init_kt_constants(L.buf[0].KT, tid, 64 * NWAVE_SEG);
   init_kt_constants(L.buf[1].KT, tid, 64 * NWAVE_SEG);
-  StageRegs st;
+  // two chunks of loads in flight: chunk c + 1 sits in registers while chunk c is processed
+  StageRegs sa, sb;
   StageConv cv;
+  const int last = c0 + nch - 1;
   if (stager) {
-    stage_load<VEC_V, false>(st, p, nullptr, kh, vh, c0 * CH, lane, w);
-    stage_convert<false>(st, cv, p.alpha, p.beta);
-    stage_write<false>(cv, nullptr, nullptr, nullptr, L.buf[0].KT, L.buf[0].VT, lane, w);
+    stage_load<VEC_V, false>(sa, p, nullptr, kh, vh, c0 * CH, lane, w);
+    stage_load<VEC_V, false>(sb, p, nullptr, kh, vh, min(c0 + 1, last) * CH, lane, w, nch > 1);
+    stage_convert<false>(sa, cv, p.alpha, p.beta, lane);
+    stage_write<false>(cv, nullptr, nullptr, L.buf[0].KT, L.buf[0].VT, lane, w);
   }
   lds_barrier();
-  for (int c = 0; c < nch; ++c) {
+  auto step = [&](int c, StageRegs& nxt, StageRegs& ahead) {
+    // nxt holds chunk c + 1; ahead (free) receives chunk c + 2.  Issued by every wave (empty for
+    // the non-staging one) so that the wait for nxt below counts only older loads.
+    stage_load<VEC_V, false>(ahead, p, nullptr, kh, vh, min(c0 + c + 2, last) * CH, lane, w, stager && c + 2 < nch);
     const SegTables& T = L.buf[c & 1];
-    if (stager && c + 1 < nch) stage_load<VEC_V, false>(st, p, nullptr, kh, vh, (c0 + c + 1) * CH, lane, w);
     update_blocks<1>(T.KT, T.VT, S, ra, rb, r, h);
     gram_update(T.KT, G, grow, h, w, NWAVE_SEG);
     if (stager && c + 1 < nch) {
       SegTables& U = L.buf[(c + 1) & 1];
-      stage_convert<false>(st, cv, p.alpha, p.beta);
+      stage_convert<false>(nxt, cv, p.alpha, p.beta, lane);
       stage_pin<false>(cv);
-      stage_write<false>(cv, nullptr, nullptr, nullptr, U.KT, U.VT, lane, w);
+      stage_write<false>(cv, nullptr, nullptr, U.KT, U.VT, lane, w);
     }
     lds_barrier();
+  };
+  for (int c = 0; c < nch; c += 2) {
+    step(c, sb, sa);
+    if (c + 1 < nch) step(c + 1, sa, sb);
   }
   // increment: S^T fp16 [dv][slot]; Gram partials of the waves summed through LDS
   const size_t slot = (size_t)bh * p.P + seg;
   uint16_t* ws = p.wsS + slot * (64 * NF);
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
+  for (int n = 0; n < (active ? 2 : 0); ++n) {
 #pragma unroll
     for (int J = 0; J < 2; ++J) {
       const f32x16& a = S[0][n];
@@ -444,7 +470,7 @@ __global__ __launch_bounds__(64 * NWAVE_SEG) void chunked_segment_kernel(const C
   for (int e = 0; e < 16; e += 4)
     *reinterpret_cast<f32x4*>(&red[(w * 64 + lane) * 16 + e]) = (f32x4){G[e], G[e + 1], G[e + 2], G[e + 3]};
   lds_barrier();
-  if (w == 0) {
+  if (w == 0 && active) {
     float* gout = p.wsG + slot * 1024 + lane * 16;
 #pragma unroll
     for (int e = 0; e < 16; e += 4) {
@@ -458,47 +484,44 @@ __global__ __launch_bounds__(64 * NWAVE_SEG) void chunked_segment_kernel(const C
 
 // -------------------------------------------------------------------------------------------
 // Kernel 2: exclusive prefixes over segments, in place: afterwards slot p - 1 holds the sum of
-// the increments of segments 0 .. p-1.  Thread (head, 16-byte unit); fp32 accumulation.
+// the increments of segments 0 .. p-1.  Thread (head, 8-byte unit), fp32 accumulation, the loads
+// of up to 16 segments in flight at once.
 __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p) {
-  constexpr int US = 64 * NF / 8, UG = 1024 / 4;   // 16-byte units of S^T (fp16) and G (fp32)
+  constexpr int US = 64 * NF / 4, UG = 1024 / 2;   // 8-byte units of S^T (fp16) and G (fp32)
   const int e = blockIdx.x * 256 + threadIdx.x, bh = blockIdx.y;
   const int nseg = p.P - 1;
   if (e < US) {
-    uint16_t* base = p.wsS + (size_t)bh * p.P * (64 * NF) + 8 * (size_t)e;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < nseg; s0 += 8) {
-      u32x4 x[8];
+    uint16_t* base = p.wsS + (size_t)bh * p.P * (64 * NF) + 4 * (size_t)e;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < nseg; s0 += 16) {
+      u32x2 x[16];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        x[i] = s0 + i < nseg ? *reinterpret_cast<const u32x4*>(base + (size_t)(s0 + i) * (64 * NF))
-                             : (u32x4){0u, 0u, 0u, 0u};
+      for (int i = 0; i < 16; ++i)
+        x[i] = s0 + i < nseg ? *reinterpret_cast<const u32x2*>(base + (size_t)(s0 + i) * (64 * NF)) : (u32x2){0u, 0u};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 16; ++i) {
         if (s0 + i >= nseg) break;
-        u32x4 o;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[2 * j] += f16_lo_to_f32(x[i][j]);
-          acc[2 * j + 1] += f16_hi_to_f32(x[i][j]);
-          o[j] = pack_f16x2(acc[2 * j], acc[2 * j + 1]);
-        }
-        *reinterpret_cast<u32x4*>(base + (size_t)(s0 + i) * (64 * NF)) = o;
+        acc[0] += f16_lo_to_f32(x[i][0]);
+        acc[1] += f16_hi_to_f32(x[i][0]);
+        acc[2] += f16_lo_to_f32(x[i][1]);
+        acc[3] += f16_hi_to_f32(x[i][1]);
+        *reinterpret_cast<u32x2*>(base + (size_t)(s0 + i) * (64 * NF)) =
+            (u32x2){pack_f16x2(acc[0], acc[1]), pack_f16x2(acc[2], acc[3])};
       }
     }
   } else if (e < US + UG) {
-    float* base = p.wsG + (size_t)bh * p.P * 1024 + 4 * (size_t)(e - US);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < nseg; s0 += 8) {
-      f32x4 x[8];
+    float* base = p.wsG + (size_t)bh * p.P * 1024 + 2 * (size_t)(e - US);
+    f32x2 acc = {0.f, 0.f};
+    for (int s0 = 0; s0 < nseg; s0 += 16) {
+      f32x2 x[16];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        x[i] = s0 + i < nseg ? *reinterpret_cast<const f32x4*>(base + (size_t)(s0 + i) * 1024)
-                             : (f32x4){0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < 16; ++i)
+        x[i] = s0 + i < nseg ? *reinterpret_cast<const f32x2*>(base + (size_t)(s0 + i) * 1024) : (f32x2){0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 16; ++i) {
         if (s0 + i >= nseg) break;
         acc += x[i];
-        *reinterpret_cast<f32x4*>(base + (size_t)(s0 + i) * 1024) = acc;
+        *reinterpret_cast<f32x2*>(base + (size_t)(s0 + i) * 1024) = acc;
       }
     }
   }
@@ -626,29 +649,30 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
   init_kt_constants(L.KT, tid, 64 * NWAVE_OUT);
   publish_state<NB>(L, S, OB::first, r, h);
   if (GRAM) publish_gram(L, G, r, h);
-  stage_convert<true>(st, cv, p.alpha, p.beta);
-  stage_write<true>(cv, L.Q0, L.Q1, L.Kr, L.KT, L.VT, lane, W);
+  stage_convert<true>(st, cv, p.alpha, p.beta, lane);
+  stage_write<true>(cv, L.Q0, L.Kr, L.KT, L.VT, lane, W);
   lds_barrier();
 
   constexpr u32 kOnes = 0x3c003c00u;
   for (int c = 0; c < nch; ++c) {
     const int row0 = (c0 + c) * CH;
-    // next chunk (unconditional, which keeps the chunk body one basic block: past the end of the
-    // segment it reads the next segment's tokens or, past N, zeros, and the values go unused)
-    stage_load<VEC, true>(st, p, qh, kh, vh, min(row0 + CH, N - 1), lane, W);
+    // next chunk, issued unconditionally (one basic block); after the last chunk it reads nothing
+    stage_load<VEC, true>(st, p, qh, kh, vh, min(row0 + CH, N - 1), lane, W, c + 1 < nch);
 
     // ---- phi(q) of token 32W + r (lane half h: q~ rotated by 2h elements) and the
     // inter-chunk product O^T += S^T phi(Q)^T
-    u32 R[8];
+    u32 R[8], R2[8];
     {
-      const uint16_t* qrow = (h ? L.Q1 : L.Q0) + (32 * W + r) * QRS;
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(qrow);
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(qrow + 8);
+      // elements 4h .. 4h + 15 of the extended row: q~ rotated by 2h register pairs
+      const uint16_t* qrow = L.Q0 + (32 * W + r) * QRS + 4 * h;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        R[i] = a0[i];
-        R[4 + i] = a1[i];
+        const u32x2 a = *reinterpret_cast<const u32x2*>(qrow + 4 * i);
+        R[2 * i] = a[0];
+        R[2 * i + 1] = a[1];
       }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) R2[i] = pk_mul_f16(R[i], 0x40004000u);
     }
     f32x16 O[2] = {splat16(0.f), splat16(0.f)};
 #pragma unroll
@@ -659,14 +683,14 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
         const Tpl t = tpl(4 * kk + m);
         u32 v;
         if (t.t == TL) {
-          v = R[t.a];
+          v = R2[t.a];
         } else if (t.t == TS) {
           v = pk_mul_f16(R[t.a], R[t.a]);
         } else if (t.t == TX) {
-          v = pk_mul_f16(R[t.a], swap16(R[t.a]));
+          v = pk_mul_f16(R2[t.a], swap16(R[t.a]));
           if (t.a == 0) v = (v & 0xffffu) | 0x3c000000u;
         } else {
-          v = pk_mul_f16(R[t.a], t.sw ? swap16(R[t.b]) : R[t.b]);
+          v = pk_mul_f16(R2[t.a], t.sw ? swap16(R[t.b]) : R[t.b]);
         }
         bq[m] = v;
       }
@@ -718,7 +742,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
         const u32x4 bp = {pk[4 * s], pk[4 * s + 1], pk[4 * s + 2], pk[4 * s + 3]};
 #pragma unroll
         for (int n = 0; n < 2; ++n) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(&L.VT[(32 * n + r) * KRS + 32 * j + 16 * s + 8 * h]);
+          const u32x4 a = *reinterpret_cast<const u32x4*>(&L.VT[vt_off(32 * n + r, 4 * j + 2 * s + h)]);
           O[n] = mfma32x32x16_f16(a, bp, O[n]);
         }
       }
@@ -775,12 +799,12 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
     // ---- state update with this chunk
     update_blocks<NB>(L.KT, L.VT, S, ra, rb, r, h);
     if (GRAM) gram_update(L.KT, G, grow, h, 0, 1);
-    stage_convert<true>(st, cv, p.alpha, p.beta);   // next chunk, in registers
+    stage_convert<true>(st, cv, p.alpha, p.beta, lane);   // next chunk, in registers
     stage_pin<true>(cv);
 
     lds_barrier();   // every wave is done with this chunk's tables and the published state
     if (c + 1 < nch) {
-      stage_write<true>(cv, L.Q0, L.Q1, L.Kr, L.KT, L.VT, lane, W);
+      stage_write<true>(cv, L.Q0, L.Kr, L.KT, L.VT, lane, W);
       publish_state<NB>(L, S, OB::first, r, h);
       if (GRAM) publish_gram(L, G, r, h);
       lds_barrier();
@@ -893,25 +917,26 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
   const double rc = sqrt((double)a.scale);
   p.alpha = (float)(rc * ldexp(1.0, sigma / 2));
   p.beta = (float)(rc * ldexp(1.0, -sigma / 2));
-  // internal k side -> reference features: constant 2, linear 2 k~, square k~^2, pair 2 k~ k~
+  // internal k side -> reference features: constant 2, linear k~, square k~^2, pair k~ k~
   p.st_fac[0] = 0.5f;
-  p.st_fac[1] = (float)(ldexp(1.0, sigma / 2) * 0.5);
+  p.st_fac[1] = (float)ldexp(1.0, sigma / 2);
   p.st_fac[2] = (float)(ldexp(1.0, sigma) / sqrt(2.0));
-  p.st_fac[3] = (float)(ldexp(1.0, sigma) * 0.5);
+  p.st_fac[3] = (float)ldexp(1.0, sigma);
   p.eps = a.eps;
   p.normalize = a.normalize ? 1 : 0;
   p.out_f32 = a.out_f32 ? 1 : 0;
   const bool vec_v = (a.dv % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 15) == 0);
   p.vec_out = (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0);
   if (P > 1) {
-    const dim3 grid((unsigned)(a.BH * (P - 1)));
+    const dim3 grid((unsigned)((a.BH * (P - 1) + SEG_PER_WG - 1) / SEG_PER_WG));
+    const dim3 block(64 * NWAVE_SEG * SEG_PER_WG);
     if (vec_v)
-      hipLaunchKernelGGL(chunked_segment_kernel<true>, grid, dim3(64 * NWAVE_SEG), 0, stream, p);
+      hipLaunchKernelGGL(chunked_segment_kernel<true>, grid, block, 0, stream, p);
     else
-      hipLaunchKernelGGL(chunked_segment_kernel<false>, grid, dim3(64 * NWAVE_SEG), 0, stream, p);
+      hipLaunchKernelGGL(chunked_segment_kernel<false>, grid, block, 0, stream, p);
     int e = (int)hipGetLastError();
     if (e != 0) return e;
-    const dim3 pgrid((unsigned)((64 * NF / 8 + 1024 / 4 + 255) / 256), (unsigned)a.BH);
+    const dim3 pgrid((unsigned)((64 * NF / 4 + 1024 / 2 + 255) / 256), (unsigned)a.BH);
     hipLaunchKernelGGL(chunked_prefix_kernel, pgrid, dim3(256), 0, stream, p);
     e = (int)hipGetLastError();
     if (e != 0) return e;
