@@ -34,7 +34,8 @@ struct SlidingParams {
 };
 
 template <int KS, int MT, int QT, bool VEC>
-__global__ __launch_bounds__(256) void sliding_bf16_kernel(const SlidingParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 8 ? 1 : 2))) void sliding_bf16_kernel(
+    const SlidingParams p) {
   constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128 * QT;
   constexpr int KROW = DK + 8;
   using Stager = BlockStager<KS, MT, VEC>;
@@ -79,15 +80,20 @@ __global__ __launch_bounds__(256) void sliding_bf16_kernel(const SlidingParams p
     lrun[qt] = 0.f;
   }
 
-  Stager st;
-  st.load(kg, vg, jlo * BN, N, d, dv, tid);
-  st.store(Ks[0], VTs[0], tid);
+  // Two key blocks of loads in flight: block j + 1 waits in registers while block j is used.
+  // Look-ahead loads past jhi are issued with no rows in range (they touch no memory), so that
+  // the loop body has no wave-uniform branches around loads and the wait for block j + 1 does not
+  // drain the newer loads.
+  Stager sa, sb;
+  sa.load(kg, vg, jlo * BN, N, d, dv, tid);
+  sb.load(kg, vg, (jlo + 1) * BN, jlo + 1 <= jhi ? N : 0, d, dv, tid);
+  sa.store(Ks[0], VTs[0], tid);
   __syncthreads();
 
   const float sl2 = p.scale_log2;
-  for (int j = jlo; j <= jhi; ++j) {
+  auto block_step = [&](int j, Stager& nxt, Stager& ahead) {
     const int s = (j - jlo) & 1;
-    if (j < jhi) st.load(kg, vg, (j + 1) * BN, N, d, dv, tid);
+    ahead.load(kg, vg, (j + 2) * BN, j + 2 <= jhi ? N : 0, d, dv, tid);
 
     if (wave_live) {
 #pragma unroll
@@ -169,8 +175,12 @@ __global__ __launch_bounds__(256) void sliding_bf16_kernel(const SlidingParams p
         }
       }
     }
-    if (j < jhi) st.store(Ks[s ^ 1], VTs[s ^ 1], tid);
+    if (j < jhi) nxt.store(Ks[s ^ 1], VTs[s ^ 1], tid);
     __syncthreads();
+  };
+  for (int j = jlo; j <= jhi; j += 2) {
+    block_step(j, sb, sa);
+    if (j + 1 <= jhi) block_step(j + 1, sa, sb);
   }
 
   if (!wave_live) return;
@@ -207,7 +217,7 @@ int launch_sl(SlidingParams p, bool vec, hipStream_t stream) {
 template <int KS>
 int dispatch_sl_mt(const SlidingParams& p, bool vec, hipStream_t stream) {
   if (p.dv <= 32) return launch_sl<KS, 1, 2>(p, vec, stream);
-  if (p.dv <= 64) return launch_sl<KS, 2, 2>(p, vec, stream);
+  if (p.dv <= 64) return launch_sl<KS, 2, 1>(p, vec, stream);
   return launch_sl<KS, 4, 1>(p, vec, stream);
 }
 
