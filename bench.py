@@ -129,8 +129,8 @@ class Call:
             self.ws_bytes = nb
             self.ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=q.device) if nb else None
             if main_only:
-                # the attention kernel alone: V pre-pass done once here, outside the timed calls
-                rc = self.L.la_based_parallel_pack(v.data_ptr(), self.dt, B, H, N, d, dv,
+                # the attention kernel alone: K/V pre-pass done once here, outside the timed calls
+                rc = self.L.la_based_parallel_pack(k.data_ptr(), v.data_ptr(), self.dt, B, H, N, d, dv,
                                                    self.ws.data_ptr() if self.ws is not None else None, self.ws_bytes,
                                                    self.stream)
                 _lib.check(rc, "la_based_parallel_pack")

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 2
+#define LA_ABI_VERSION 3
 
 /* element types */
 #define LA_F32 0
@@ -57,8 +57,9 @@ const char* la_status_string(int status);
  * q, k: (B,H,N,d); v, out: (B,H,N,dv); in_dtype / out_dtype: LA_BF16 or LA_F32 (q, k and v
  * share in_dtype).  den_or_null: optional (B,H,N) fp32 output of den_t (without eps).
  * workspace: device scratch of at least la_based_parallel_workspace_bytes(...) bytes, 16-byte
- * aligned (may be NULL when that is 0).  It holds V repacked as fp16 V^T blocks for the
- * bf16, d = 16, dv % 8 == 0, dv <= 64 kernel; its contents on return are unspecified.
+ * aligned (may be NULL when that is 0).  It holds V repacked as fp16 V^T blocks and prefix
+ * sums over 64-key blocks of the column sums of V, of k and of k k^T for the bf16, d = 16,
+ * dv % 8 == 0, dv <= 64 kernel; its contents on return are unspecified.
  * Limits: 1 <= d <= 128, 1 <= dv <= 128, scale > 0 and finite, eps >= 0 and finite.
  * The reference passes scale = 1/sqrt(d) and eps = 1e-6.
  */
@@ -70,16 +71,16 @@ int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dt
                           void* workspace, size_t workspace_bytes, void* hip_stream);
 
 /*
- * The two halves of la_based_parallel_fwd for shapes that use the workspace: the V pre-pass,
- * and the attention kernel reading a workspace that already holds the pre-pass of the same v
- * (several calls with one v, or timing the attention kernel alone).  No counterpart in the
+ * The two halves of la_based_parallel_fwd for shapes that use the workspace: the K/V pre-pass,
+ * and the attention kernel reading a workspace that already holds the pre-pass of the same k
+ * and v (several calls with one k and v, or timing the attention kernel alone).  No counterpart in the
  * reference, whose parallel kernel has no pre-pass (kernels/nki_attention.py:33-115).  For
  * shapes with la_based_parallel_workspace_bytes(...) == 0 the pack is a no-op and
  * la_based_parallel_fwd_packed is la_based_parallel_fwd.  The packed kernels need q, k, out
  * 16-byte and v 8-byte aligned (LA_ERR_BAD_ALIGNMENT otherwise; la_based_parallel_fwd instead
  * falls back to its unpacked kernel).
  */
-int la_based_parallel_pack(const void* v, int in_dtype, int B, int H, int N, int d, int dv,
+int la_based_parallel_pack(const void* k, const void* v, int in_dtype, int B, int H, int N, int d, int dv,
                            void* workspace, size_t workspace_bytes, void* hip_stream);
 int la_based_parallel_fwd_packed(const void* q, const void* k, const void* v, int in_dtype,
                                  void* out, int out_dtype, float* den_or_null,

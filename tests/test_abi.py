@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib()
-    assert lib.la_abi_version() == 2
+    assert lib.la_abi_version() == 3
     for code in range(-8, 1):
         s = lib.la_status_string(code).decode()
         assert s and s != "unknown status"
@@ -86,10 +86,12 @@ def test_parallel_pack_and_packed_argument_errors():
     lib = _lib()
     need = lib.la_based_parallel_workspace_bytes(1, 1, 8, 16, 64, 1)
     pack = lib.la_based_parallel_pack
-    assert pack(None, 1, 1, 1, 8, 16, 64, P, need, None) == -1
-    assert pack(P, 1, 1, 1, 8, 16, 64, None, need, None) == -6
-    assert pack(ctypes.c_void_p(24), 1, 1, 1, 8, 16, 64, P, need, None) == -8   # v not 16-byte aligned
-    assert pack(P, 0, 1, 1, 8, 16, 64, None, 0, None) == 0                       # fp32: nothing to pack
+    assert pack(None, P, 1, 1, 1, 8, 16, 64, P, need, None) == -1
+    assert pack(P, None, 1, 1, 1, 8, 16, 64, P, need, None) == -1
+    assert pack(P, P, 1, 1, 1, 8, 16, 64, None, need, None) == -6
+    assert pack(ctypes.c_void_p(24), P, 1, 1, 1, 8, 16, 64, P, need, None) == -8   # k not 16-byte aligned
+    assert pack(P, ctypes.c_void_p(20), 1, 1, 1, 8, 16, 64, P, need, None) == -8   # v not 8-byte aligned
+    assert pack(P, P, 0, 1, 1, 8, 16, 64, None, 0, None) == 0                       # fp32: nothing to pack
     f = lib.la_based_parallel_fwd_packed
     a = [P, P, P, 1, P, 1, None, 1, 1, 8, 16, 64, 0.25, 1e-6, 1, P, need, None]
     a_bad = list(a)
@@ -104,9 +106,9 @@ def test_parallel_workspace_sizes():
     lib = _lib()
     ws = lib.la_based_parallel_workspace_bytes
     # per (b, h) and 64-key block: fp16 V^T (dv rows padded to 68 keys, whole 1 KB units) and
-    # the fp32 column sums of V
-    assert ws(2, 16, 8192, 16, 64, 1) == 32 * 128 * (9216 + 256)
-    assert ws(1, 1, 65, 16, 32, 1) == 2 * (5120 + 128)
+    # an fp32 record of statistics (column sums of V, sums of k, the k k^T triangle, padding)
+    assert ws(2, 16, 8192, 16, 64, 1) == 32 * 128 * (9216 + 4 * (64 + 160))
+    assert ws(1, 1, 65, 16, 32, 1) == 2 * (5120 + 4 * (32 + 160))
     assert ws(1, 1, 64, 16, 64, 0) == 0        # fp32 inputs: no workspace
     assert ws(1, 1, 64, 32, 64, 1) == 0        # d != 16
     assert ws(1, 1, 64, 16, 60, 1) == 0        # dv % 8 != 0

@@ -175,7 +175,7 @@ def test_single_hip_runtime_and_native_library():
 @pytest.mark.parametrize("B,H,N,dv", [(1, 2, 777, 64), (2, 8, 1024, 32)])
 def test_pack_then_packed_kernel_equals_fused_call(B, H, N, dv):
     """la_based_parallel_pack + la_based_parallel_fwd_packed is la_based_parallel_fwd, bit for
-    bit, including a second v packed into the same workspace."""
+    bit, including a second k and v packed into the same workspace."""
     from kernels import _lib
     L = _lib.lib()
     d = 16
@@ -194,7 +194,8 @@ def test_pack_then_packed_kernel_equals_fused_call(B, H, N, dv):
             if mode == "fused":
                 assert L.la_based_parallel_fwd(*args) == 0
             else:
-                assert L.la_based_parallel_pack(v.data_ptr(), 1, B, H, N, d, dv, ws.data_ptr(), ws_bytes, st) == 0
+                assert L.la_based_parallel_pack(k.data_ptr(), v.data_ptr(), 1, B, H, N, d, dv, ws.data_ptr(),
+                                                ws_bytes, st) == 0
                 assert L.la_based_parallel_fwd_packed(*args) == 0
             outs.append((out, den))
         torch.cuda.synchronize()

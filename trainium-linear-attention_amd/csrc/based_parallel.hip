@@ -52,7 +52,8 @@ struct ParallelParams {
   const uint16_t* k;
   const uint16_t* v;
   const uint16_t* vt;     // packed fp16 V^T blocks (packed path), [BH][nb64][vt_block]
-  const float* vpre;      // packed path: exclusive prefix over blocks of the column sums of V, [BH][nb64][DV]
+  const float* stats;     // packed path: exclusive prefixes over blocks of the block statistics,
+                          // [BH][nb64][stats_width(DV)] (V column sums, k sums, k k^T triangle)
   void* out;
   float* den;
   int BH, N, d, dv, nqb, nb64;
@@ -70,60 +71,6 @@ using VtBlockP = VtBlock<DV, VROW>;
 size_t vt_block_bytes(int dv) { return dv <= 32 ? (size_t)VtBlockP<32>::bytes : (size_t)VtBlockP<64>::bytes; }
 
 bool packed_shape(int d, int dv) { return d == 16 && dv % 8 == 0 && dv <= 64; }
-
-// colsum[bh][blk][DV] -> exclusive prefix over blk, in place.  One work-group per head; the
-// head's column sums go through LDS in tiles of 4096 values (all loads of a tile in flight at
-// once), NQ threads per column scan a tile, and a carry links the tiles.
-template <int DV>
-__global__ __launch_bounds__(256) void colsum_scan_kernel(float* __restrict__ colsum, int nb64) {
-  constexpr int TB = 4096 / DV;   // blocks per tile
-  constexpr int NQ = 256 / DV;    // threads per column
-  constexpr int PER = TB / NQ;    // blocks per thread and tile
-  __shared__ float tile[TB * DV];
-  __shared__ float tot[NQ][DV];
-  const int tid = threadIdx.x, col = tid % DV, qi = tid / DV;
-  float* __restrict__ c = colsum + (size_t)blockIdx.x * nb64 * DV;
-  float carry = 0.f;
-  for (int t0 = 0; t0 < nb64; t0 += TB) {
-    const int nt = min(TB, nb64 - t0);
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {   // all loads in flight before the first LDS store
-      const int idx = tid + 256 * i;
-      x[i] = idx < nt * DV ? c[(size_t)t0 * DV + idx] : 0.f;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) tile[tid + 256 * i] = x[i];
-    __syncthreads();
-    float part = 0.f;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int bl = qi * PER + i;
-      if (bl < nt) part += tile[bl * DV + col];
-    }
-    tot[qi][col] = part;
-    __syncthreads();
-    float run = carry, all = carry;
-#pragma unroll
-    for (int q2 = 0; q2 < NQ; ++q2) {
-      if (q2 < qi) run += tot[q2][col];
-      all += tot[q2][col];
-    }
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int bl = qi * PER + i;
-      if (bl < nt) {
-        const float x = tile[bl * DV + col];
-        tile[bl * DV + col] = run;
-        run += x;
-      }
-    }
-    __syncthreads();
-    for (int idx = tid; idx < nt * DV; idx += 256) c[(size_t)t0 * DV + idx] = tile[idx];
-    carry = all;
-    __syncthreads();
-  }
-}
 
 // UNIT: 1/c scales to exactly 1 (scale = 1/sqrt(d) with d a power of 4), so the score MFMA
 // starts from the inline constant 1.0 and u = b*b - 1.
@@ -167,10 +114,11 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   const int jd = wq0 / BN;             // this wave's diagonal key block
   const bool wave_live = wq0 < N;
 
-  // Q fragments (B operand of S^T = K Q^T): lane holds q[query][16kk + 8h .. +7].
+  // Q fragments (B operand of S^T = K Q^T): lane holds q[query][16kk + 8h .. +7].  The packed
+  // path copies them through LDS in its prologue.
   u32x4 qf[QT][KS];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
+  for (int qt = 0; qt < QT && !PACKED; ++qt) {
     const int query = wq0 + 32 * qt + n;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
@@ -201,12 +149,19 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) rsum[qt] = 0.f;
 
+  const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
+
+  // Packed path: the row sums of u over the keys before the diagonal block come from the block
+  // statistics instead of the key loop: with x = q~ (this query, all 16 dims) and a = x.k,
+  //   sum_k u = sum_k (a^2 + 2 a / c) = x^T (sum_k k k^T) x + (2 / c) x.(sum_k k).
+  float rs_pre[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) rs_pre[qt] = 0.f;
+
   // running column sum of V over blocks [0, jb0 + s) for snapshot s: thread -> (row, segment)
   const int vs_row = tid / LPR, vs_seg = tid % LPR;
   float vacc = 0.f;
   constexpr u32 kOnes = 0x3c003c00u;  // packed fp16 (1, 1)
-
-  const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
 
   // ---- packed path: global -> LDS copies.  Wave wu owns units wu, wu + NW, ... of every
   // block; unit u lands at byte 1024 u of the stage (K units 0-1, V^T units 2..).
@@ -228,17 +183,20 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       uoff[i] = 1024 * (u - 2) + 16 * lane;
     }
   }
+  // Copy i of this wave for block blk (unit wu + NW i; nothing if this wave has no unit i).
+  // Blocks past the last one read out of range (zero bytes from memory) into the stage they
+  // would use, which holds no live block, so that a wave issues the same number of copies per
+  // block whatever nblk is.
+  auto issue_unit = [&](int blk, int i) {
+    const int u = wu + NW * i;
+    if (NW * (i + 1) > NU && u >= NU) return;
+    const bool isk = u < 2;
+    const int off = blk < nblk ? uoff[i] + blk * (isk ? BN * 32 : VTB) : kOffOutOfRange;
+    lds_copy16(isk ? rk : rv, lds_addr(&stage[blk % NRAW][0]) + 1024 * u, off);
+  };
   auto issue = [&](int blk) {
-    const u32 base = lds_addr(&stage[blk % NRAW][0]);
 #pragma unroll
-    for (int i = 0; i < UPW; ++i) {
-      const int u = wu + NW * i;
-      if (u >= NU) break;
-      if (u < 2)
-        lds_copy16(rk, base + 1024 * u, uoff[i] + blk * (BN * 32));
-      else
-        lds_copy16(rv, base + 1024 * u, uoff[i] + blk * VTB);
-    }
+    for (int i = 0; i < UPW; ++i) issue_unit(blk, i);
   };
   // LDS-only barrier: this wave's LDS operations done, then s_barrier; the empty asm
   // statements keep the compiler from moving memory operations across it.
@@ -298,6 +256,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       }
     }
   };
+  // (the packed path takes the row sums of full blocks from the block statistics)
   auto elementwise = [&](const f32x16 (&b)[2][QT], u32x4 (&pf)[2][QT][2]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
@@ -310,19 +269,20 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             const int i = 8 * m + 2 * c;
-            const float x0 = b[ks][qt][i], x1 = b[ks][qt][i + 1];
-            wv[c] = pack_f16x2(__builtin_fmaf(x0, x0, -inv_c2), __builtin_fmaf(x1, x1, -inv_c2));
-            r = dot2_f16(wv[c], kOnes, r);
+            wv[c] = sq_plus_f16x2(b[ks][qt][i], b[ks][qt][i + 1], -inv_c2);
+            if (!PACKED) r = dot2_f16(wv[c], kOnes, r);
           }
           pf[ks][qt][m] = (u32x4){wv[0], wv[1], wv[2], wv[3]};
         }
         rsum[qt] = r;
       }
   };
-  auto pv = [&](int j, const u32x4 (&pf)[2][QT][2]) {
+  // cb >= 0: issue this wave's copy 1 of block cb between the two key halves
+  auto pv = [&](int j, const u32x4 (&pf)[2][QT][2], int cb) {
     const uint16_t* vt = vtile(j);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 2; ++ks) {
+      if (PACKED && ks == 1 && cb >= 0) issue_unit(cb, 1);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -334,20 +294,67 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) acc[qt][mt] = mfma32x32x16_f16(vf, pf[ks][qt][m], acc[qt][mt]);
         }
+    }
   };
 
   Stager st;
   if (PACKED) {
-    // drain the Q loads so that vmcnt counts only copies from here on
-    __builtin_amdgcn_s_waitcnt(0x0f70);
-    const int issued = min(NRAW - 3, nblk - 1);
+    // Blocks 0 .. NRAW - 3 now, then two per loop iteration, spread over its two block steps.
+    // With blocks 0 and 1, each wave copies its 64 Q rows (2 KB, contiguous) and the
+    // statistics record of its diagonal block (1 KB) into stages NRAW - 2 and NRAW - 1 (one
+    // 12 KB region: Q rows of the four waves, then their records); both stages are refilled
+    // only after the barrier below.  Queries >= N and the records of waves past the end read
+    // out of range, as zeros.
+    constexpr int SW = stats_width(DV);
+    static_assert(NW == 4 && 2 * STAGE * 2 >= 4 * 3072, "Q rows and records fit in two stages");
+    issue(0);
+    issue(1);
+    const u32x4 rq = buffer_rsrc(qg, (u32)N * 32u);
+    const u32x4 rst = buffer_rsrc(p.stats + (size_t)bh * p.nb64 * SW, (u32)p.nb64 * (u32)(SW * 4));
+    const uint16_t* region = &stage[0][0] + (NRAW - 2) * STAGE;
+    const u32 qlds = lds_addr(region) + 2048 * wu, slds = lds_addr(region) + 8192 + 1024 * wu;
+    lds_copy16(rq, qlds, wq0 * 32 + 16 * lane);
+    lds_copy16(rq, qlds + 1024, wq0 * 32 + 1024 + 16 * lane);
+    lds_copy16(rst, slds, jd * (SW * 4) + 16 * lane);
 #pragma unroll
-    for (int b = 0; b <= NRAW - 3; ++b)
-      if (b <= issued) issue(b);
-    wait_copies(my_units * (issued - min(1, nblk - 1)));   // blocks 0 and 1 landed
+    for (int b = 2; b <= NRAW - 3; ++b) issue(b);
+    wait_copies(my_units * (NRAW - 4));   // blocks 0 and 1, this wave's Q rows and record landed
+    const uint16_t* qs = region + 1024 * wu;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+      qf[qt][0] = scale_bf16x8(*reinterpret_cast<const u32x4*>(qs + (32 * qt + n) * 16 + 8 * h), p.qscale);
+    if (wave_live) {
+      const float* st = reinterpret_cast<const float*>(region + 4096 + 512 * wu) + DV;
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        u32 lo[4], hi[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const u32 own = qf[qt][0][c], oth = (u32)__shfl_xor((int)own, 32);
+          lo[c] = h ? oth : own;
+          hi[c] = h ? own : oth;
+        }
+        float x[16];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          x[2 * c] = bf16_lo_to_f32(lo[c]);
+          x[2 * c + 1] = bf16_hi_to_f32(lo[c]);
+          x[8 + 2 * c] = bf16_lo_to_f32(hi[c]);
+          x[9 + 2 * c] = bf16_hi_to_f32(hi[c]);
+        }
+        float r = 0.f;
+        int t = kStatK2;
+#pragma unroll
+        for (int a = 0; a < 16; ++a) {
+          float sa = 2.f * inv_c * st[kStatK1 + a];
+#pragma unroll
+          for (int b = a; b < 16; ++b) sa = __builtin_fmaf(st[t++], x[b], sa);
+          r = __builtin_fmaf(x[a], sa, r);
+        }
+        rs_pre[qt] = r;
+      }
+    }
     lds_barrier();
-    if (NRAW - 2 < nblk) issue(NRAW - 2);
-    if (NRAW - 1 < nblk) issue(NRAW - 1);
   } else {
     st.load(kg, vg, 0, N, d, dv, tid);
     st.store(Ks[0], VTs[0], tid);
@@ -355,8 +362,8 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
     __syncthreads();
   }
 
-  // One key block of the loop.
-  auto block_step = [&](int j) {
+  // One key block of the loop; packed path: also this wave's copies of block cb.
+  auto block_step = [&](int j, int cb) {
     if (!PACKED && j <= jb0 + NSNAP - 2) {
       const uint16_t* vt = vtile(j);
       const uint16_t* src = vt + vs_row * VROW + vs_seg * KPL;
@@ -376,9 +383,16 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       f32x16 b[2][QT];
       u32x4 pf[2][QT][2];
       scores(j, b);
+      if (PACKED) issue_unit(cb, 0);
       elementwise(b, pf);
-      pv(j, pf);
-    } else if (wave_live && j == jd) {
+      pv(j, pf, PACKED ? cb : -1);
+#pragma unroll
+      for (int i = 2; i < UPW; ++i)
+        if (PACKED) issue_unit(cb, i);
+      return;
+    }
+    if (PACKED) issue(cb);
+    if (wave_live && j == jd) {
       // Diagonal block: causal mask on u, plus the exact "1" of p through a mask MFMA.
       const uint16_t* vt = vtile(j);
 #pragma unroll
@@ -471,22 +485,20 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   if (PACKED) {
     for (int j = 0; j < nblk; j += 2) {
       if (j >= 2) {
-        // iterations j and j+1 read blocks j and j+1; stages of blocks j-2 and j-1 are free
-        // after the barrier
-        const int issued = min(j + NRAW - 3, nblk - 1);
-        wait_copies(my_units * max(0, issued - min(j + 1, nblk - 1)));
+        // blocks up to j + NRAW - 3 issued; j and j + 1 must have landed.  The steps read
+        // blocks j and j + 1 and refill the stages of blocks j - 2 and j - 1, free after the
+        // barrier.
+        wait_copies(my_units * (NRAW - 4));
         lds_barrier();
-        if (j + NRAW - 2 < nblk) issue(j + NRAW - 2);
-        if (j + NRAW - 1 < nblk) issue(j + NRAW - 1);
       }
-      block_step(j);
-      if (j + 1 < nblk) block_step(j + 1);
+      block_step(j, j + NRAW - 2);
+      if (j + 1 < nblk) block_step(j + 1, j + NRAW - 1);
     }
     lds_barrier();
   } else {
     for (int j = 0; j < nblk; ++j) {
       if (j + 1 < nblk) st.load(kg, vg, (j + 1) * BN, N, d, dv, tid);
-      block_step(j);
+      block_step(j, -1);
       if (j + 1 < nblk) st.store(Ks[(j & 1) ^ 1], VTs[(j & 1) ^ 1], tid);
       __syncthreads();
     }
@@ -505,7 +517,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       const int row = 32 * mt + c32_row(i, h);
       float t = 0.f;
       if (PACKED) {
-        t = p.vpre[((size_t)bh * p.nb64 + jd) * DV + row];
+        t = p.stats[((size_t)bh * p.nb64 + jd) * stats_width(DV) + row];
       } else {
 #pragma unroll
         for (int sg = 0; sg < LPR; ++sg) t += snap[si][row * LPR + sg];
@@ -516,7 +528,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   const float fscale = p.fscale;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const float rs = rsum[qt] + __shfl_xor(rsum[qt], 32);
+    const float rs = rsum[qt] + __shfl_xor(rsum[qt], 32) + rs_pre[qt];
     const int query = wq0 + 32 * qt + n;
     if (query >= N) continue;
     const float den = (float)(query + 1) + fscale * rs;
@@ -564,10 +576,11 @@ int launch_packed(const ParallelParams& pp, int stages, hipStream_t stream) {
   ParallelParams p = pp;
   p.nqb = (p.N + BM - 1) / BM;
   if (stages & 1) {
-    hipLaunchKernelGGL((vt_pack_kernel<DV, VROW, true, true>), dim3((unsigned)p.nb64, (unsigned)p.BH), dim3(256), 0,
-                       stream, p.v, const_cast<uint16_t*>(p.vt), const_cast<float*>(p.vpre), p.N, p.dv, p.nb64);
-    hipLaunchKernelGGL((colsum_scan_kernel<DV>), dim3((unsigned)p.BH), dim3(256), 0, stream,
-                       const_cast<float*>(p.vpre), p.nb64);
+    hipLaunchKernelGGL((par_pack_kernel<DV, VROW, true>), dim3((unsigned)p.nb64, (unsigned)p.BH), dim3(256), 0,
+                       stream, p.k, p.v, const_cast<uint16_t*>(p.vt), const_cast<float*>(p.stats), p.N, p.dv,
+                       p.nb64);
+    hipLaunchKernelGGL(stats_scan_kernel, dim3((unsigned)p.BH, (unsigned)(stats_width(DV) / 16)), dim3(256), 0,
+                       stream, const_cast<float*>(p.stats), p.nb64, stats_width(DV));
   }
   if (stages & 2) {
     const dim3 grid((unsigned)(p.nqb * p.BH)), block(64 * NW);
@@ -610,12 +623,12 @@ int dispatch_mt(const ParallelParams& p, bool vec, bool packed, int stages, hipS
 
 }  // namespace
 
-// [V^T blocks: BH * nb64 * vt_block_bytes][column-sum prefixes: BH * nb64 * DV fp32]
+// [V^T blocks: BH * nb64 * vt_block_bytes][statistics prefixes: BH * nb64 * stats_width(DV) fp32]
 size_t parallel_workspace_bytes(int BH, int N, int d, int dv, bool in_f32) {
   if (in_f32 || !packed_shape(d, dv)) return 0;
   const size_t nb64 = ((size_t)N + BN - 1) / BN;
-  const size_t DV = dv <= 32 ? 32 : 64;
-  return (size_t)BH * nb64 * (vt_block_bytes(dv) + DV * 4);
+  const int DV = dv <= 32 ? 32 : 64;
+  return (size_t)BH * nb64 * (vt_block_bytes(dv) + (size_t)stats_width(DV) * 4);
 }
 
 int launch_based_parallel_fp32(const ParallelArgs& a, hipStream_t stream);
@@ -629,7 +642,7 @@ int launch_based_parallel(const ParallelArgs& a, hipStream_t stream) {
   p.vt = static_cast<const uint16_t*>(a.workspace);
   p.nb64 = (a.N + BN - 1) / BN;
   if (a.workspace != nullptr)
-    p.vpre = reinterpret_cast<const float*>(static_cast<const char*>(a.workspace) +
+    p.stats = reinterpret_cast<const float*>(static_cast<const char*>(a.workspace) +
                                             (size_t)a.BH * p.nb64 * vt_block_bytes(a.dv));
   p.out = a.out;
   p.den = a.den;

@@ -110,10 +110,10 @@ int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dt
                         workspace, workspace_bytes, hip_stream, 3);
 }
 
-int la_based_parallel_pack(const void* v, int in_dtype, int B, int H, int N, int d, int dv, void* workspace,
-                           size_t workspace_bytes, void* hip_stream) {
-  // q, k and out are not touched by the pre-pass; v stands in for them in the shared checks
-  return parallel_entry(v, v, v, in_dtype, const_cast<void*>(v), in_dtype, nullptr, B, H, N, d, dv, 1.0f, 0.f, 1,
+int la_based_parallel_pack(const void* k, const void* v, int in_dtype, int B, int H, int N, int d, int dv,
+                           void* workspace, size_t workspace_bytes, void* hip_stream) {
+  // q and out are not touched by the pre-pass; k stands in for them in the shared checks
+  return parallel_entry(k, k, v, in_dtype, const_cast<void*>(k), in_dtype, nullptr, B, H, N, d, dv, 1.0f, 0.f, 1,
                         workspace, workspace_bytes, hip_stream, 1);
 }
 

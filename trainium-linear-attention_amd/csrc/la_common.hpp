@@ -37,6 +37,13 @@ __device__ __forceinline__ u32 pack_f16x2(float lo, float hi) {
   return __builtin_bit_cast(u32, p);
 }
 
+// (x0*x0 + c, x1*x1 + c) as packed fp16, each rounded once from the exact product-sum
+// (the compiler selects v_fma_mixlo_f16 / v_fma_mixhi_f16 for the scalar conversions).
+__device__ __forceinline__ u32 sq_plus_f16x2(float x0, float x1, float c) {
+  const f16x2 r = {(_Float16)__builtin_fmaf(x0, x0, c), (_Float16)__builtin_fmaf(x1, x1, c)};
+  return __builtin_bit_cast(u32, r);
+}
+
 __device__ __forceinline__ float f16_lo_to_f32(u32 w) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
 }

@@ -34,8 +34,8 @@ _SIGNATURES = {
     "la_based_parallel_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_void,
                                        _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int,
                                        _c_void, _c_size, _c_void]),
-    "la_based_parallel_pack": (_c_int, [_c_void, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void, _c_size,
-                                        _c_void]),
+    "la_based_parallel_pack": (_c_int, [_c_void, _c_void, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void,
+                                        _c_size, _c_void]),
     "la_based_parallel_fwd_packed": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_void,
                                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int,
                                               _c_void, _c_size, _c_void]),
@@ -48,7 +48,7 @@ _SIGNATURES = {
     "la_taylor_feature_map": (_c_int, [_c_void, _c_int, _c_void, _c_int, ctypes.c_longlong, _c_int, _c_void]),
 }
 
-EXPECTED_ABI = 2
+EXPECTED_ABI = 3
 
 
 class BasedLAError(RuntimeError):
