@@ -38,6 +38,8 @@
 // blocks ahead, and synchronises the work-group once per two blocks.  Barriers are plain
 // s_barrier with explicit vmcnt / lgkmcnt waits so that in-flight copies are not drained.
 // Other shapes stage K and V through registers into a double-buffered LDS block.
+#include <type_traits>
+
 #include "la_common.hpp"
 #include "la_internal.hpp"
 #include "la_pack.hpp"
@@ -494,6 +496,8 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       block_step(j, j + NRAW - 2);
       if (j + 1 < nblk) block_step(j + 1, j + NRAW - 1);
     }
+    // every copy of every wave landed (the output tiles below reuse the stages)
+    wait_copies(0);
     lds_barrier();
   } else {
     for (int j = 0; j < nblk; ++j) {
@@ -526,6 +530,50 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
     }
 
   const float fscale = p.fscale;
+  if (PACKED) {
+    // The wave's output tile (64 queries x DV) goes through its own part of the free stages so
+    // that the stores write whole rows: lane -> (row, 16-byte chunk).
+    auto store_tile = [&](auto f32_tag) {
+      constexpr bool F32 = decltype(f32_tag)::value;
+      constexpr int EB = F32 ? 4 : 2, RB = DV * EB, RS = RB + 16, CPR = RB / 16;
+      static_assert(4 * 64 * RS <= NRAW * STAGE * 2, "output tiles fit in the stages");
+      char* tile = reinterpret_cast<char*>(&stage[0][0]) + wu * (64 * RS);
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const float rs = rsum[qt] + __shfl_xor(rsum[qt], 32) + rs_pre[qt];
+        const int query = wq0 + 32 * qt + n;
+        const float den = (float)(query + 1) + fscale * rs;
+        const float inv = p.normalize ? 1.0f / (den + p.eps) : 1.0f;
+        if (p.den != nullptr && h == 0 && query < N) p.den[hrow + query] = den;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = (fscale * acc[qt][mt][4 * g + e] + vsum[mt][4 * g + e]) * inv;
+            char* dst = tile + (32 * qt + n) * RS + (32 * mt + 8 * g + 4 * h) * EB;
+            if (F32)
+              *reinterpret_cast<f32x4*>(dst) = (f32x4){y[0], y[1], y[2], y[3]};
+            else
+              *reinterpret_cast<u32x2*>(dst) = (u32x2){pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+          }
+      }
+      const int rowbytes = dv * EB;
+      char* out = static_cast<char*>(p.out) + (hrow + wq0) * (size_t)rowbytes;
+#pragma unroll
+      for (int it = 0; it < CPR; ++it) {
+        const int idx = 64 * it + lane, r = idx / CPR, c = idx % CPR;
+        const u32x4 x = *reinterpret_cast<const u32x4*>(tile + r * RS + 16 * c);
+        if (wq0 + r < N && 16 * c < rowbytes) *reinterpret_cast<u32x4*>(out + (size_t)r * rowbytes + 16 * c) = x;
+      }
+    };
+    if (p.out_f32)
+      store_tile(std::true_type{});
+    else
+      store_tile(std::false_type{});
+    return;
+  }
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const float rs = rsum[qt] + __shfl_xor(rsum[qt], 32) + rs_pre[qt];
