@@ -364,6 +364,68 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
     __syncthreads();
   }
 
+  // Packed path, two full blocks j and j + 1 as four 32-key halves u = 0..3, software
+  // pipelined so that the elementwise step of half u + 1 (VALU) runs beside the P.V MFMAs of
+  // half u: scores(u + 2) are issued before pv(u), elementwise(u + 1) after it.  Also this
+  // wave's copies of blocks cb0 and cb1.
+  auto pair_step = [&](int j, int cb0, int cb1) {
+    f32x16 b[4][QT];
+    u32x4 pf[4][QT][2];
+    auto S = [&](int u) {
+      const u32x4 kf = kfrag(j + (u >> 1), u & 1, 0);
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) b[u][qt] = mfma32x32x16(kf, qf[qt][0], splat16(inv_c));
+    };
+    auto E = [&](int u) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          u32 wv[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            wv[c] = sq_plus_f16x2(b[u][qt][8 * m + 2 * c], b[u][qt][8 * m + 2 * c + 1], -inv_c2);
+          pf[u][qt][m] = (u32x4){wv[0], wv[1], wv[2], wv[3]};
+        }
+    };
+    auto P = [&](int u) {
+      const uint16_t* vt = vtile(j + (u >> 1));
+      const int ks = u & 1;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const uint16_t* vp = vt + (32 * mt + n) * VROW + 32 * ks + 16 * m + 4 * h;
+          const u32x2 a0 = *reinterpret_cast<const u32x2*>(vp);
+          const u32x2 a1 = *reinterpret_cast<const u32x2*>(vp + 8);
+          const u32x4 vf = {a0[0], a0[1], a1[0], a1[1]};
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) acc[qt][mt] = mfma32x32x16_f16(vf, pf[u][qt][m], acc[qt][mt]);
+        }
+    };
+    S(0);
+    S(1);
+    issue_unit(cb0, 0);
+    E(0);
+    S(2);
+    P(0);
+    E(1);
+    issue_unit(cb0, 1);
+    S(3);
+    P(1);
+    E(2);
+    issue_unit(cb1, 0);
+    P(2);
+    E(3);
+    issue_unit(cb1, 1);
+    P(3);
+#pragma unroll
+    for (int i = 2; i < UPW; ++i) {
+      issue_unit(cb0, i);
+      issue_unit(cb1, i);
+    }
+  };
+
   // One key block of the loop; packed path: also this wave's copies of block cb.
   auto block_step = [&](int j, int cb) {
     if (!PACKED && j <= jb0 + NSNAP - 2) {
@@ -493,8 +555,12 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
         wait_copies(my_units * (NRAW - 4));
         lds_barrier();
       }
-      block_step(j, j + NRAW - 2);
-      if (j + 1 < nblk) block_step(j + 1, j + NRAW - 1);
+      if (wave_live && j + 1 < jd) {
+        pair_step(j, j + NRAW - 2, j + NRAW - 1);
+      } else {
+        block_step(j, j + NRAW - 2);
+        if (j + 1 < nblk) block_step(j + 1, j + NRAW - 1);
+      }
     }
     // every copy of every wave landed (the output tiles below reuse the stages)
     wait_copies(0);
