@@ -97,6 +97,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t VTs[PACKED ? 1 : 2][PACKED ? 8 : DV * VROW];
   __shared__ __attribute__((aligned(16))) uint16_t stage[PACKED ? NRAW : 1][PACKED ? STAGE : 8];
   __shared__ __attribute__((aligned(16))) float snap[PACKED ? 1 : NSNAP][PACKED ? 4 : DV * LPR];
+  __shared__ __attribute__((aligned(16))) float vsl[PACKED ? NW : 1][PACKED ? DV : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
@@ -152,13 +153,6 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   for (int qt = 0; qt < QT; ++qt) rsum[qt] = 0.f;
 
   const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
-
-  // Packed path: the row sums of u over the keys before the diagonal block come from the block
-  // statistics instead of the key loop: with x = q~ (this query, all 16 dims) and a = x.k,
-  //   sum_k u = sum_k (a^2 + 2 a / c) = x^T (sum_k k k^T) x + (2 / c) x.(sum_k k).
-  float rs_pre[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) rs_pre[qt] = 0.f;
 
   // running column sum of V over blocks [0, jb0 + s) for snapshot s: thread -> (row, segment)
   const int vs_row = tid / LPR, vs_seg = tid % LPR;
@@ -325,10 +319,35 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt)
       qf[qt][0] = scale_bf16x8(*reinterpret_cast<const u32x4*>(qs + (32 * qt + n) * 16 + 8 * h), p.qscale);
+    const float* rec = reinterpret_cast<const float*>(region + 4096 + 512 * wu);
+    if (lane < DV) vsl[wu][lane] = rec[lane];   // column sums of V, for the epilogue
     if (wave_live) {
-      const float* st = reinterpret_cast<const float*>(region + 4096 + 512 * wu) + DV;
+      // Row sums of u over the blocks before the diagonal block, x = q~ (the query's 16 dims):
+      // x^T U x + (2/c) x.k1 with U the k k^T prefix as an upper-triangular matrix (off-diagonal
+      // entries doubled).  U x for 32 queries is one MFMA pass with U (rows 16..31 zero),
+      // split into bf16 hi + lo, as the A operand and Q^T as B; each lane then dots its 8 rows
+      // of U x with x, and the two lane halves' partial sums go into rsum (added in the
+      // epilogue).
+      const float* k1 = rec + DV + kStatK1;
+      const float* tri = rec + DV + kStatK2;
+      u32x4 ahi, alo;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float v2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int b = 8 * h + 2 * c + e;
+          const bool ok = n < 16 && b >= n;
+          v2[e] = ok ? tri[ok ? 16 * n - n * (n - 1) / 2 + b - n : 0] : 0.f;
+        }
+        const u32 hi = pack_bf16x2(v2[0], v2[1]);
+        ahi[c] = hi;
+        alo[c] = pack_bf16x2(v2[0] - bf16_lo_to_f32(hi), v2[1] - bf16_hi_to_f32(hi));
+      }
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
+        f32x16 ux = mfma32x32x16(ahi, qf[qt][0], splat16(0.f));
+        ux = mfma32x32x16(alo, qf[qt][0], ux);
         u32 lo[4], hi[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -345,15 +364,13 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
           x[9 + 2 * c] = bf16_hi_to_f32(hi[c]);
         }
         float r = 0.f;
-        int t = kStatK2;
 #pragma unroll
-        for (int a = 0; a < 16; ++a) {
-          float sa = 2.f * inv_c * st[kStatK1 + a];
-#pragma unroll
-          for (int b = a; b < 16; ++b) sa = __builtin_fmaf(st[t++], x[b], sa);
-          r = __builtin_fmaf(x[a], sa, r);
+        for (int i = 0; i < 8; ++i) {   // rows a = c32_row(i, h) < 16 of this lane
+          const int a0 = 8 * (i >> 2) + (i & 3);
+          const float xa = h ? x[a0 + 4] : x[a0];
+          r = __builtin_fmaf(xa, __builtin_fmaf(2.f * inv_c, k1[c32_row(i, h)], ux[i]), r);
         }
-        rs_pre[qt] = r;
+        rsum[qt] = r;
       }
     }
     lds_barrier();
@@ -587,7 +604,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       const int row = 32 * mt + c32_row(i, h);
       float t = 0.f;
       if (PACKED) {
-        t = p.stats[((size_t)bh * p.nb64 + jd) * stats_width(DV) + row];
+        t = vsl[wu][row];
       } else {
 #pragma unroll
         for (int sg = 0; sg < LPR; ++sg) t += snap[si][row * LPR + sg];
@@ -606,7 +623,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       char* tile = reinterpret_cast<char*>(&stage[0][0]) + wu * (64 * RS);
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
-        const float rs = rsum[qt] + __shfl_xor(rsum[qt], 32) + rs_pre[qt];
+        const float rs = rsum[qt] + __shfl_xor(rsum[qt], 32);
         const int query = wq0 + 32 * qt + n;
         const float den = (float)(query + 1) + fscale * rs;
         const float inv = p.normalize ? 1.0f / (den + p.eps) : 1.0f;
@@ -642,7 +659,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   }
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const float rs = rsum[qt] + __shfl_xor(rsum[qt], 32) + rs_pre[qt];
+    const float rs = rsum[qt] + __shfl_xor(rsum[qt], 32);
     const int query = wq0 + 32 * qt + n;
     if (query >= N) continue;
     const float den = (float)(query + 1) + fscale * rs;
