@@ -707,7 +707,8 @@ int launch_packed(const ParallelParams& pp, int stages, hipStream_t stream) {
   ParallelParams p = pp;
   p.nqb = (p.N + BM - 1) / BM;
   if (stages & 1) {
-    hipLaunchKernelGGL((par_pack_kernel<DV, VROW, true>), dim3((unsigned)p.nb64, (unsigned)p.BH), dim3(256), 0,
+    hipLaunchKernelGGL((par_pack_kernel<DV, VROW>), dim3((unsigned)((p.nb64 + PPW - 1) / PPW), (unsigned)p.BH),
+                       dim3(256), 0,
                        stream, p.k, p.v, const_cast<uint16_t*>(p.vt), const_cast<float*>(p.stats), p.N, p.dv,
                        p.nb64);
     hipLaunchKernelGGL(stats_scan_kernel, dim3((unsigned)p.BH, (unsigned)(stats_width(DV) / 16)), dim3(256), 0,

@@ -25,100 +25,125 @@ constexpr int kStatK2 = 16;    // offset of the k k^T triangle after the V colum
 constexpr int kTri = 136;      // entries of the triangle (16 * 17 / 2)
 __host__ __device__ constexpr int stats_width(int DV) { return DV + 160; }
 
-// One work-group per (64-key block, head); k rows are d = 16 bf16 (8-byte aligned).  Zero for
-// keys >= N, rows >= dv and the padding.  VEC: dv even and v 4-byte aligned (pairs of V are
-// loaded as one dword).
-template <int DV, int ROW, bool VEC>
+// One work-group per PPW consecutive 64-key blocks of a head (all their loads issued first); k
+// rows are d = 16 bf16 (16-byte aligned), v rows dv % 8 == 0 bf16 (8-byte aligned).  Per block:
+//  * V^T: thread t takes keys 2 (t / CPR) and 2 (t / CPR) + 1, columns 8 (t % CPR) .. +7, so it
+//    holds both halves of 8 fp16 pairs of the transposed block; it writes them into an LDS
+//    image of the block (padding zero), which whole-chunk stores then copy out;
+//  * column sums of V from the same registers: lane shuffles, then the waves through LDS;
+//  * k sums and the k k^T triangle from one 32x32x16 MFMA chain over the 64 keys (wave 0):
+//    A = K^T (rows 16..31 zero), B = K with a column of ones at 16, so C[a][b] = (k k^T)[a][b]
+//    and C[a][16] = k1[a].
+constexpr int PPW = 1;   // blocks per pack work-group
+
+template <int DV, int ROW>
 __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                        uint16_t* __restrict__ vt, float* __restrict__ stats, int N,
                                                        int dv, int nb64) {
-  constexpr int NP = 256 / DV;   // partial sums per column
   constexpr int SW = stats_width(DV);
-  __shared__ float tile[BN][DV + 1];
-  __shared__ float ktile[BN][17];
-  __shared__ float part[NP][DV];
-  const int blk = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
-  const int row0 = blk * BN;
-  const uint16_t* __restrict__ src = v + ((size_t)bh * N + row0) * dv;
-  constexpr int NLD = BN * (DV / 2) / 256;   // element pairs per thread
-  u32 x[NLD];
+  constexpr int CPR = DV / 8;                 // 8-element column groups per V row
+  constexpr int NT = (BN / 2) * CPR;          // threads holding a (key pair, column group)
+  constexpr int NWV = NT / 64;                // waves among them
+  constexpr int IMG = VtBlock<DV, ROW>::bytes;
+  static_assert(ROW % 2 == 0 && NT <= 256, "pack layout");
+  __shared__ __attribute__((aligned(16))) u32 img[IMG / 4];
+  __shared__ __attribute__((aligned(16))) uint16_t kl[BN * 16];
+  __shared__ float csum[NWV][DV];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int bh = blockIdx.y, blk0 = blockIdx.x * PPW;
+  const int nb = min(PPW, nb64 - blk0);
+  const int kp = tid / CPR, cg = tid % CPR, col = 8 * cg;
+
+  for (int i = tid; i < IMG / 16; i += 256) reinterpret_cast<u32x4*>(img)[i] = (u32x4){0u, 0u, 0u, 0u};
+
+  u32x4 va[PPW], vb[PPW], kx[PPW];
 #pragma unroll
-  for (int i = 0; i < NLD; ++i) {   // all loads in flight before the first LDS store
-    const int idx = tid + 256 * i, key = idx / (DV / 2), col = 2 * (idx % (DV / 2));
-    u32 e = 0u;
-    if (row0 + key < N) {
-      const uint16_t* s = src + (size_t)key * dv + col;
-      if (VEC) {
-        if (col < dv) e = *reinterpret_cast<const u32*>(s);
-      } else {
-        e = (col < dv ? (u32)s[0] : 0u) | (col + 1 < dv ? (u32)s[1] << 16 : 0u);
+  for (int b = 0; b < PPW; ++b) {
+    const int row0 = (blk0 + b) * BN;
+    u32x4 x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
+    if (b < nb && tid < NT && col < dv) {
+      const uint16_t* src = v + ((size_t)bh * N + row0 + 2 * kp) * dv + col;
+      if (row0 + 2 * kp < N) {
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(src), hi = *reinterpret_cast<const u32x2*>(src + 4);
+        x0 = (u32x4){lo[0], lo[1], hi[0], hi[1]};
+      }
+      if (row0 + 2 * kp + 1 < N) {
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(src + dv), hi = *reinterpret_cast<const u32x2*>(src + dv + 4);
+        x1 = (u32x4){lo[0], lo[1], hi[0], hi[1]};
       }
     }
-    x[i] = e;
+    va[b] = x0;
+    vb[b] = x1;
+    u32x4 y = {0u, 0u, 0u, 0u};
+    if (b < nb && tid < 128 && row0 + (tid >> 1) < N)
+      y = *reinterpret_cast<const u32x4*>(k + ((size_t)bh * N + row0 + (tid >> 1)) * 16 + 8 * (tid & 1));
+    kx[b] = y;
   }
-  // k: thread -> key tid / 4, dims 4 (tid % 4) .. +3
-  u32x2 kx = {0u, 0u};
-  {
-    const int key = tid >> 2;
-    if (row0 + key < N)
-      kx = *reinterpret_cast<const u32x2*>(k + ((size_t)bh * N + row0 + key) * 16 + 4 * (tid & 3));
-  }
+
 #pragma unroll
-  for (int i = 0; i < NLD; ++i) {
-    const int idx = tid + 256 * i, key = idx / (DV / 2), col = 2 * (idx % (DV / 2));
-    tile[key][col] = bf16_lo_to_f32(x[i]);
-    tile[key][col + 1] = bf16_hi_to_f32(x[i]);
-  }
-  {
-    float* kr = &ktile[tid >> 2][4 * (tid & 3)];
-    kr[0] = bf16_lo_to_f32(kx[0]);
-    kr[1] = bf16_hi_to_f32(kx[0]);
-    kr[2] = bf16_lo_to_f32(kx[1]);
-    kr[3] = bf16_hi_to_f32(kx[1]);
-  }
-  __syncthreads();
-  u32* __restrict__ dst = reinterpret_cast<u32*>(vt + ((size_t)bh * nb64 + blk) * (VtBlock<DV, ROW>::bytes / 2));
-  for (int idx = tid; idx < VtBlock<DV, ROW>::bytes / 4; idx += 256) {
-    const int row = (2 * idx) / ROW, col = (2 * idx) % ROW;
-    u32 y = 0u;
-    if (row < DV && col < BN) y = pack_f16x2(tile[col][row], tile[col + 1][row]);
-    dst[idx] = y;
-  }
-  float* __restrict__ rec = stats + ((size_t)bh * nb64 + blk) * SW;
-  {
-    const int col = tid % DV, pi = tid / DV;
-    float t = 0.f;
+  for (int b = 0; b < PPW; ++b) {
+    if (b >= nb) break;
+    const int blk = blk0 + b;
+    __syncthreads();   // image zeroed / the previous block's readers done
+    float part[8];
+    if (tid < NT) {
 #pragma unroll
-    for (int key = pi * (BN / NP); key < (pi + 1) * (BN / NP); ++key) t += tile[key][col];
-    part[pi][col] = t;
-  }
-  if (tid < kTri) {
-    // triangle entry tid -> (a, b), a <= b, row-major
-    int a = 0, t = tid;
-    while (t >= 16 - a) {
-      t -= 16 - a;
-      ++a;
+      for (int e = 0; e < 8; ++e) {
+        const u32 a0 = va[b][e >> 1], a1 = vb[b][e >> 1];
+        const float f0 = (e & 1) ? bf16_hi_to_f32(a0) : bf16_lo_to_f32(a0);
+        const float f1 = (e & 1) ? bf16_hi_to_f32(a1) : bf16_lo_to_f32(a1);
+        part[e] = f0 + f1;
+        img[(col + e) * (ROW / 2) + kp] = pack_f16x2(f0, f1);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[e] = 0.f;
     }
-    const int b = a + t;
-    float s = 0.f;
-#pragma unroll 16
-    for (int key = 0; key < BN; ++key) s = __builtin_fmaf(ktile[key][a], ktile[key][b], s);
-    rec[DV + kStatK2 + tid] = a == b ? s : 2.f * s;
-  } else if (tid < kTri + 16) {
-    const int a = tid - kTri;
-    float s = 0.f;
-#pragma unroll 16
-    for (int key = 0; key < BN; ++key) s += ktile[key][a];
-    rec[DV + kStatK1 + a] = s;
-  } else if (tid < kTri + 24) {
-    rec[DV + kStatK2 + kTri + (tid - kTri - 16)] = 0.f;
-  }
-  __syncthreads();
-  if (tid < DV) {
-    float t = 0.f;
+    if (tid < 128) *reinterpret_cast<u32x4*>(&kl[8 * tid]) = kx[b];
+    // column sums: lanes with the same column group differ by multiples of CPR
 #pragma unroll
-    for (int pi = 0; pi < NP; ++pi) t += part[pi][tid];
-    rec[tid] = t;
+    for (int sh = CPR; sh < 64; sh <<= 1)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[e] += __shfl_xor(part[e], sh);
+    if (w < NWV && lane < CPR) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) csum[w][8 * lane + e] = part[e];
+    }
+    __syncthreads();
+    u32* dst = reinterpret_cast<u32*>(vt + ((size_t)bh * nb64 + blk) * (IMG / 2));
+    for (int i = tid; i < IMG / 16; i += 256) reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(img)[i];
+    float* __restrict__ rec = stats + ((size_t)bh * nb64 + blk) * SW;
+    if (tid < DV) {
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < NWV; ++i) t += csum[i][tid];
+      rec[tid] = t;
+    }
+    if (w == NWV % 4) {
+      const int nn = lane & 31, h = lane >> 5;
+      f32x16 acc = splat16(0.f);
+#pragma unroll
+      for (int k0 = 0; k0 < BN; k0 += 16) {
+        u32 av[4], bv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = k0 + 8 * h + 2 * i;
+          const int c = nn < 16 ? nn : 0;
+          const u32 x0 = kl[key * 16 + c], x1 = kl[(key + 1) * 16 + c];
+          av[i] = nn < 16 ? (x0 | (x1 << 16)) : 0u;
+          bv[i] = nn == 16 ? 0x3f803f80u : av[i];   // bf16 (1, 1)
+        }
+        acc = mfma32x32x16((u32x4){av[0], av[1], av[2], av[3]}, (u32x4){bv[0], bv[1], bv[2], bv[3]}, acc);
+      }
+      // lane: column nn, rows c32_row(i, h) (< 16 for i < 8)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int a = c32_row(i, h);
+        if (nn < 16 && a <= nn) rec[DV + kStatK2 + 16 * a - a * (a - 1) / 2 + nn - a] = a == nn ? acc[i] : 2.f * acc[i];
+        if (nn == 16) rec[DV + kStatK1 + a] = acc[i];
+      }
+      if (lane < 8) rec[DV + kStatK2 + kTri + lane] = 0.f;
+    }
   }
 }
 
