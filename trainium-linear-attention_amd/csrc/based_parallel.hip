@@ -348,26 +348,20 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       for (int qt = 0; qt < QT; ++qt) {
         f32x16 ux = mfma32x32x16(ahi, qf[qt][0], splat16(0.f));
         ux = mfma32x32x16(alo, qf[qt][0], ux);
-        u32 lo[4], hi[4];
+        // this lane's rows a = c32_row(i, h), i < 8, are dims 4h .. 4h+3 and 8+4h .. 8+4h+3: the
+        // lane's own q~ holds dims 8h .. 8h+7, its partner (lane ^ 32) the other eight
+        u32 own[4], oth[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const u32 own = qf[qt][0][c], oth = (u32)__shfl_xor((int)own, 32);
-          lo[c] = h ? oth : own;
-          hi[c] = h ? own : oth;
+          own[c] = qf[qt][0][c];
+          oth[c] = (u32)__shfl_xor((int)own[c], 32);
         }
-        float x[16];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          x[2 * c] = bf16_lo_to_f32(lo[c]);
-          x[2 * c + 1] = bf16_hi_to_f32(lo[c]);
-          x[8 + 2 * c] = bf16_lo_to_f32(hi[c]);
-          x[9 + 2 * c] = bf16_hi_to_f32(hi[c]);
-        }
+        const u32 xr[4] = {h ? oth[2] : own[0], h ? oth[3] : own[1], h ? own[2] : oth[0], h ? own[3] : oth[1]};
         float r = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {   // rows a = c32_row(i, h) < 16 of this lane
-          const int a0 = 8 * (i >> 2) + (i & 3);
-          const float xa = h ? x[a0 + 4] : x[a0];
+        for (int i = 0; i < 8; ++i) {
+          const u32 wv = xr[i >> 1];
+          const float xa = (i & 1) ? bf16_hi_to_f32(wv) : bf16_lo_to_f32(wv);
           r = __builtin_fmaf(xa, __builtin_fmaf(2.f * inv_c, k1[c32_row(i, h)], ux[i]), r);
         }
         rsum[qt] = r;
