@@ -34,7 +34,7 @@ struct SlidingParams {
 };
 
 template <int KS, int MT, int QT, bool VEC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 8 ? 1 : 2))) void sliding_bf16_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 8 ? 1 : (KS == 4 && MT == 2 && QT == 1 ? 4 : 2)))) void sliding_bf16_kernel(
     const SlidingParams p) {
   constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128 * QT;
   constexpr int KROW = DK + 8;
@@ -84,16 +84,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 8 ? 1
   // Look-ahead loads past jhi are issued with no rows in range (they touch no memory), so that
   // the loop body has no wave-uniform branches around loads and the wait for block j + 1 does not
   // drain the newer loads.
-  Stager sa, sb;
+  Stager sa;
   sa.load(kg, vg, jlo * BN, N, d, dv, tid);
-  sb.load(kg, vg, (jlo + 1) * BN, jlo + 1 <= jhi ? N : 0, d, dv, tid);
   sa.store(Ks[0], VTs[0], tid);
   __syncthreads();
 
   const float sl2 = p.scale_log2;
-  auto block_step = [&](int j, Stager& nxt, Stager& ahead) {
+  auto block_step = [&](int j, Stager& nxt) {
     const int s = (j - jlo) & 1;
-    ahead.load(kg, vg, (j + 2) * BN, j + 2 <= jhi ? N : 0, d, dv, tid);
+    nxt.load(kg, vg, (j + 1) * BN, j + 1 <= jhi ? N : 0, d, dv, tid);
 
     if (wave_live) {
 #pragma unroll
@@ -178,10 +177,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 8 ? 1
     if (j < jhi) nxt.store(Ks[s ^ 1], VTs[s ^ 1], tid);
     __syncthreads();
   };
-  for (int j = jlo; j <= jhi; j += 2) {
-    block_step(j, sb, sa);
-    if (j + 1 <= jhi) block_step(j + 1, sa, sb);
-  }
+  for (int j = jlo; j <= jhi; ++j) block_step(j, sa);
 
   if (!wave_live) return;
 #pragma unroll
