@@ -209,18 +209,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 8 ? 1
 // group reads row k0 + r, columns c0 + 4 c .. +3 and lane i ends up with column c0 + i of rows
 // k0 .. k0 + 3.  Everything else (masking, online softmax, hi/lo split of P) is as in
 // sliding_bf16_kernel.
-constexpr int kResBlocks = 3;
 
 __device__ __forceinline__ int swz_k(int row, int nch) { return row % nch; }
 __device__ __forceinline__ int swz_v(int row, int nch) { return (row >> 1) % nch; }
 
-template <int KS, int MT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void sliding_resident_kernel(
+template <int KS, int MT, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 4 : 3))) void sliding_resident_kernel(
     const SlidingParams p) {
-  constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128;
+  constexpr int DK = 16 * KS, DV = 32 * MT, BM = 32 * NW;
+  constexpr int kResBlocks = BM / BN + 1;   // key blocks a tile needs for W <= 65
   constexpr int KCH = DK / 8, VCH = DV / 8;                 // 16-byte chunks per K / V row
   constexpr int KU = BN * DK * 2 / 1024, VU = BN * DV * 2 / 1024;   // 1 KB copy units per block
-  constexpr int NU = kResBlocks * (KU + VU), UPW = (NU + 3) / 4;
+  constexpr int NU = kResBlocks * (KU + VU), UPW = (NU + NW - 1) / NW;
   static_assert((KCH & (KCH - 1)) == 0 && (VCH & (VCH - 1)) == 0, "XOR swizzle needs power-of-two rows");
   __shared__ __attribute__((aligned(16))) uint16_t Kl[kResBlocks][BN * DK];
   __shared__ __attribute__((aligned(16))) uint16_t Vl[kResBlocks][BN * DV];
@@ -240,14 +240,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void s
   const uint16_t* __restrict__ kg = p.k + hrow * DK;
   const uint16_t* __restrict__ vg = p.v + hrow * DV;
 
-  // copies: unit u (wave w takes u = w, w + 4, ...) is K unit u (blocks of KU) or V unit u - 3 KU;
+  // copies: unit u (wave w takes u = w, w + NW, ...) is K unit u (blocks of KU) or V unit
+  // u - kResBlocks KU;
   // lane l of a unit fills 16-byte slot 64 part + l of its block, i.e. row slot / nch, position
   // slot % nch, which holds chunk position ^ swizzle(row) of that row
   {
     const u32x4 rk = buffer_rsrc(kg, (u32)N * (u32)(DK * 2)), rv = buffer_rsrc(vg, (u32)N * (u32)(DV * 2));
 #pragma unroll
     for (int i = 0; i < UPW; ++i) {
-      const int u = w + 4 * i;
+      const int u = w + NW * i;
       if (u >= NU) break;
       const bool isk = u < kResBlocks * KU;
       const int uu = isk ? u : u - kResBlocks * KU;
@@ -395,8 +396,10 @@ int launch_sl(SlidingParams p, bool vec, hipStream_t stream) {
 
 template <int KS, int MT>
 int launch_resident(SlidingParams p, hipStream_t stream) {
-  p.nqb = (p.N + 127) / 128;
-  hipLaunchKernelGGL((sliding_resident_kernel<KS, MT>), dim3((unsigned)(p.nqb * p.BH)), dim3(256), 0, stream, p);
+  constexpr int NW = 8;
+  p.nqb = (p.N + 32 * NW - 1) / (32 * NW);
+  hipLaunchKernelGGL((sliding_resident_kernel<KS, MT, NW>), dim3((unsigned)(p.nqb * p.BH)), dim3(64 * NW), 0, stream,
+                     p);
   return (int)hipGetLastError();
 }
 
