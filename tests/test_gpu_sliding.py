@@ -76,3 +76,31 @@ def test_config4_bf16():
     assert e < TOL_BF16
     y16 = K.nki_sliding_window_attn(*to_dev(q, k, v), window_size=cfg.window)
     assert y16.dtype == torch.bfloat16 and torch.equal(y16, y.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("d,dv", [(16, 32), (16, 64), (32, 32), (32, 64), (64, 32), (64, 64)])
+@pytest.mark.parametrize("W", [1, 37, 64, 65])
+def test_resident_window_shapes(d, dv, W):
+    """W <= 65 with d in {16, 32, 64} and dv in {32, 64} runs the LDS-resident kernel; ragged N
+    so that the last 256-query tile and its key blocks are partial."""
+    K = _kernels()
+    q, k, v = rand_qkv(1, 3, 333, d, dv, seed=d * 7 + dv + W, dtype=torch.bfloat16)
+    y = K.sliding_window_attn(*to_dev(q, k, v), window_size=W, out_dtype=torch.float32)
+    want = ref.sliding_dense(q, k, v, window_size=W)
+    assert err(y, want) < TOL_BF16
+
+
+def test_resident_matches_streaming_path():
+    """The same inputs through the resident kernel (16-byte aligned) and through the streaming
+    kernel (q moved off 16-byte alignment, which the resident kernel requires)."""
+    K = _kernels()
+    q, k, v = to_dev(*rand_qkv(2, 2, 700, 64, 64, seed=9, dtype=torch.bfloat16))
+    y_res = K.sliding_window_attn(q, k, v, window_size=64, out_dtype=torch.float32)
+    buf = torch.empty(q.numel() + 4, dtype=q.dtype, device=q.device)
+    q_off = buf[4:].view(q.shape)
+    q_off.copy_(q)
+    assert q_off.data_ptr() % 16 != 0
+    y_str = K.sliding_window_attn(q_off, k, v, window_size=64, out_dtype=torch.float32)
+    want = ref.sliding_dense(q.cpu(), k.cpu(), v.cpu(), window_size=64)
+    assert err(y_res, want) < TOL_BF16 and err(y_str, want) < TOL_BF16
+    assert (y_res - y_str).abs().max().item() < 1e-3
