@@ -62,6 +62,9 @@ def parse():
                          "that scales FETCH_SIZE / WRITE_SIZE counters into HBM bytes")
     ap.add_argument("--only", default=None,
                     help="comma-separated configuration names (or 'headline') to measure alone, e.g. for profiling")
+    ap.add_argument("--crossover", action="store_true",
+                    help="only sweep sequence lengths: whole parallel forward vs chunked forward (d=16, dv=64, bf16), "
+                         "the measurement behind solution()'s dispatch threshold")
     return ap.parse_args()
 
 
@@ -214,6 +217,31 @@ def measure(cfg, steps, warmup, rotate, device, main_only=False):
     return res
 
 
+# (B, H) pairs and sequence lengths of the crossover sweep (the reference sweeps 256 .. 16384 at B=1, H=2)
+CROSSOVER_BH = [(1, 2), (2, 16), (8, 16)]
+CROSSOVER_N = [256, 512, 1024, 2048, 4096, 8192, 16384]
+
+
+def crossover(steps, warmup, rotate, device):
+    """ms per call of the whole parallel forward and of the normalised chunked forward over
+    CROSSOVER_N for each of CROSSOVER_BH, and per (B, H) the shortest length from which the
+    chunked kernel is faster at every longer length measured."""
+    rows, first = [], {}
+    for B, H in CROSSOVER_BH:
+        best = None
+        for N in CROSSOVER_N:
+            ms = {kind: measure((kind, kind, B, H, N, 16, 64, "bf16", 7, 64, 64, True), steps, warmup, rotate,
+                                device)["ms"] for kind in ("parallel", "chunked")}
+            rows.append({"B": B, "H": H, "N": N, "parallel_ms": ms["parallel"], "chunked_ms": ms["chunked"]})
+            print(json.dumps(rows[-1]), file=sys.stderr, flush=True)
+            if ms["chunked"] < ms["parallel"]:
+                best = N if best is None else best
+            else:
+                best = None
+        first[f"B{B}H{H}"] = best
+    return {"crossover": rows, "chunked_faster_from": first}
+
+
 def torch_empty_cache():
     import torch
 
@@ -275,6 +303,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": n * 4}))
+        return
+
+    if args.crossover:
+        print(json.dumps(crossover(args.steps, args.warmup, args.rotate, device)))
         return
 
     if args.only:

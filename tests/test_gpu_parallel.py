@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from oracle import reference as ref
-from tests.helpers import err, load_golden, rand_qkv, to_dev
+from tests.helpers import err, load_golden, rand_qkv, rounded_err, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -203,3 +203,24 @@ def test_pack_then_packed_kernel_equals_fused_call(B, H, N, dv):
         want, _, want_den = ref.based_dense(q.cpu(), k.cpu(), v.cpu())
         assert err(outs[1][0], want) < TOL_BF16
         assert err(outs[1][1], want_den) < TOL_BF16
+
+
+@pytest.mark.parametrize("N,d,dv,dtype", [(255, 16, 64, torch.bfloat16), (256, 16, 64, torch.bfloat16),
+                                          (1000, 16, 32, torch.bfloat16), (300, 32, 64, torch.bfloat16),
+                                          (300, 16, 64, torch.float32)])
+def test_solution_dispatch_by_length(N, d, dv, dtype):
+    """solution() runs the chunked kernel from CHUNKED_MIN_T on (bf16, d = 16, dv <= 64) and the
+    fused kernel otherwise; either way it matches the oracle."""
+    K = _kernels()
+    from kernels import chunked_attention, pytorch_attention
+    q, k, v = rand_qkv(1, 2, N, d, dv, seed=N + d, dtype=dtype, scale_qk=0.5)
+    qd, kd, vd = to_dev(q, k, v)
+    y = K.solution(qd, kd, vd)
+    chunked = N >= pytorch_attention.CHUNKED_MIN_T and chunked_attention.chunked_supported(d, dv, qd.dtype)
+    same = chunked_attention.chunked_based_attn(qd, kd, vd) if chunked else K.solution_nki(qd, kd, vd)
+    assert torch.equal(y, same)
+    want, _, _ = ref.based_dense(q, k, v)
+    if dtype == torch.bfloat16:
+        assert rounded_err(y, want) < TOL_BF16     # bf16 output
+    else:
+        assert err(y, want) < TOL_F32

@@ -100,18 +100,22 @@ def solution_nki(q, k, v, eps=1e-6):
     return based_parallel(q, k, v, eps=eps)
 
 
-# Sequence length from which the chunked (linear-time) kernel is used by ``solution``;
-# below it the fused parallel kernel is faster.  Set from the crossover measurement.
-CHUNKED_MIN_T = 1 << 62
+# Sequence length from which ``solution`` uses the chunked (linear-time) kernel.  Measured on
+# MI355X at d=16, dv=64, bf16 (B1 H2, B2 H16, B8 H16; N = 256 .. 16384, whole forward of each
+# path): the chunked forward was faster at every length, from 0.014 vs 0.015 ms at N=256 to
+# 0.084 vs 0.762 ms at B2 H16 N=16384; shorter sequences were not measured and stay on the
+# fused kernel.
+CHUNKED_MIN_T = 256
 
 
 def solution(q, k, v, eps=1e-6):
     """BASED causal attention (reference :81-92).
 
     Dispatches by sequence length between the parallel fused kernel and the chunked
-    recurrent kernel, which compute the same function; there is no PyTorch fallback.
+    recurrent kernel, which compute the same function; shapes the chunked kernel does not
+    take (d != 16, dv > 64, fp32) go to the fused kernel.  There is no PyTorch fallback.
     """
-    if q.shape[-2] >= CHUNKED_MIN_T and q.shape[-1] == 16:
+    if q.shape[-2] >= CHUNKED_MIN_T:
         from .chunked_attention import chunked_based_attn
         return chunked_based_attn(q, k, v, eps=eps)
     return based_parallel(q, k, v, eps=eps)
