@@ -62,6 +62,9 @@ def parse():
                          "that scales FETCH_SIZE / WRITE_SIZE counters into HBM bytes")
     ap.add_argument("--only", default=None,
                     help="comma-separated configuration names (or 'headline') to measure alone, e.g. for profiling")
+    ap.add_argument("--layer", action="store_true",
+                    help="only time the full BASED layer (linear attention + sliding-window softmax, the sum "
+                         "taken in the sliding kernel's store) against the two branches run and added apart")
     ap.add_argument("--crossover", action="store_true",
                     help="only sweep sequence lengths: whole parallel forward vs chunked forward (d=16, dv=64, bf16), "
                          "the measurement behind solution()'s dispatch threshold")
@@ -242,6 +245,32 @@ def crossover(steps, warmup, rotate, device):
     return {"crossover": rows, "chunked_faster_from": first}
 
 
+# full BASED layer shapes: (B, H, N, d of the linear branch, d_sw of the softmax branch, dv, window)
+LAYER_SHAPES = [(2, 16, 8192, 16, 64, 64, 64), (2, 16, 2048, 16, 64, 64, 64)]
+
+
+def layer_bench(steps, warmup, device):
+    """ms per call of kernels.based_layer_attn and of the unfused composition (solution() and
+    nki_sliding_window_attn in bf16, then a torch add), same inputs."""
+    import torch
+
+    import kernels as K
+
+    rows = []
+    for B, H, N, d, d_sw, dv, W in LAYER_SHAPES:
+        q, k, v = make_inputs(B, H, N, d, dv, "bf16", 11, True, device)
+        q_sw, k_sw, _ = make_inputs(B, H, N, d_sw, 1, "bf16", 12, False, device)
+        fused = lambda: K.based_layer_attn(q, k, v, window_size=W, q_sw=q_sw, k_sw=k_sw)
+        apart = lambda: K.solution(q, k, v) + K.nki_sliding_window_attn(q_sw, k_sw, v, window_size=W)
+        row = {"B": B, "H": H, "N": N, "d": d, "d_sw": d_sw, "dv": dv, "window": W}
+        for name, fn in (("layer_ms", fused), ("apart_ms", apart)):
+            row[name] = round(time_calls([fn], steps, warmup), 5)
+        rows.append(row)
+        del q, k, v, q_sw, k_sw
+        torch_empty_cache()
+    return {"layer": rows}
+
+
 def torch_empty_cache():
     import torch
 
@@ -303,6 +332,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": n * 4}))
+        return
+
+    if args.layer:
+        print(json.dumps(layer_bench(args.steps, args.warmup, device)))
         return
 
     if args.crossover:

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 3
+#define LA_ABI_VERSION 4
 
 /* element types */
 #define LA_F32 0
@@ -120,6 +120,19 @@ int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dty
 int la_sliding_window_fwd(const void* q, const void* k, const void* v, int in_dtype,
                           void* out, int out_dtype, int B, int H, int N, int d, int dv,
                           int window, float scale, void* hip_stream);
+
+/*
+ * Sliding-window softmax attention plus an fp32 addend, out = sliding(q, k, v) + addend: the
+ * second half of the full BASED layer, final = linear_attention + sliding_window_softmax
+ * (kernels/nki_attention_sliding.py:4-5), with the linear-attention output as the addend.  The
+ * sum is taken in fp32 in the sliding kernel's store, then rounded once to out_dtype.
+ * addend: fp32 (B,H,N,dv), 16-byte aligned; it may be out itself when out_dtype is fp32.
+ * Other arguments and limits as la_sliding_window_fwd.  (The reference computes the two
+ * branches separately and has no entry point for the sum.)
+ */
+int la_sliding_window_fwd_add(const void* q, const void* k, const void* v, int in_dtype,
+                              const float* addend, void* out, int out_dtype, int B, int H, int N,
+                              int d, int dv, int window, float scale, void* hip_stream);
 
 /*
  * BASED Taylor feature map, phi(x) = [1, x/d^(1/4), x_i^2/(sqrt(d) sqrt(2)),

@@ -15,6 +15,8 @@ It restates, line by line, the PyTorch math of the reference repository
 * ``ref_based_numerator``       -- benchmarks/chunked_attention_benchmark.py:68-76
 * ``ref_identity_numerator``    -- benchmarks/chunked_attention_benchmark.py:81-93
 * ``ref_sliding_window_attn``   -- benchmarks/sliding_attention_benchmark.py:32-56
+* ``ref_based_layer``           -- the full BASED layer of kernels/nki_attention_sliding.py:4-5,
+                                   final = linear attention + sliding-window softmax
 
 and adds the parity oracles the GPU tests compare against:
 
@@ -151,6 +153,24 @@ def ref_sliding_window_attn(q, k, v, window_size=64, eps=EPS):
     weights = torch.softmax(scores, dim=-1)
     out = torch.matmul(weights, v.float())
     return out.to(q.dtype)
+
+
+def ref_based_layer(q, k, v, window_size=64, q_sw=None, k_sw=None, eps=EPS):
+    """kernels/nki_attention_sliding.py:4-5: final = linear_attention(Q, K, V) +
+    sliding_window_softmax(Q, K, V), each branch as the reference computes it
+    (``ref_based_attn`` and ``ref_sliding_window_attn``, both in q's dtype), summed in that
+    dtype.  ``q_sw`` / ``k_sw`` give the softmax branch its own projections (default q, k)."""
+    q_sw = q if q_sw is None else q_sw
+    k_sw = k if k_sw is None else k_sw
+    return ref_based_attn(q, k, v, eps=eps) + ref_sliding_window_attn(q_sw, k_sw, v, window_size=window_size)
+
+
+def based_layer_dense(q, k, v, window_size=64, q_sw=None, k_sw=None, eps=EPS, dtype=torch.float64):
+    """The same layer in ``dtype`` on already rounded inputs: ``based_dense`` + ``sliding_dense``."""
+    q_sw = q if q_sw is None else q_sw
+    k_sw = k if k_sw is None else k_sw
+    y, _, _ = based_dense(q, k, v, eps=eps, dtype=dtype)
+    return y + sliding_dense(q_sw, k_sw, v, window_size=window_size, dtype=dtype)
 
 
 # ----------------------------------------------------------------------------------------

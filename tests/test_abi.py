@@ -27,7 +27,7 @@ def test_header_declares_expected_entry_points():
     assert _declared() == sorted([
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
         "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_fwd", "la_sliding_window_fwd",
-        "la_taylor_feature_map"])
+        "la_sliding_window_fwd_add", "la_taylor_feature_map"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib()
-    assert lib.la_abi_version() == 3
+    assert lib.la_abi_version() == 4
     for code in range(-8, 1):
         s = lib.la_status_string(code).decode()
         assert s and s != "unknown status"
@@ -80,6 +80,24 @@ def test_parallel_argument_errors():
     assert call(ws=ctypes.c_void_p(24)) == -8
     assert call(N=0) == 0          # empty: nothing to launch
     assert call(B=0) == 0
+
+
+def test_sliding_add_argument_errors():
+    lib = _lib()
+    f = lib.la_sliding_window_fwd_add
+    ok = [P, P, P, 1, P, P, 1, 1, 1, 8, 16, 64, 64, 0.25, None]
+
+    def call(i, x):
+        a = list(ok)
+        a[i] = x
+        return f(*a)
+
+    assert call(4, None) == -1                     # addend required
+    assert call(4, ctypes.c_void_p(8)) == -8       # addend not 16-byte aligned
+    assert call(0, None) == -1
+    assert call(12, 0) == -4                       # window
+    assert call(10, 129) == -5                     # d
+    assert call(9, 0) == 0                         # N = 0: nothing to launch
 
 
 def test_parallel_pack_and_packed_argument_errors():

@@ -196,6 +196,24 @@ def test_sliding_rows_are_convex_combinations():
     assert torch.allclose(ref.sliding_dense(q, k, v, window_size=7), v, rtol=1e-14)
 
 
+@pytest.mark.parametrize("w", [1, 3, 64])
+def test_layer_is_sum_of_branches_with_own_projections(w):
+    """Full BASED layer (kernels/nki_attention_sliding.py:4-5) against brute force: the linear
+    branch on (q, k, v) and the softmax branch on (q_sw, k_sw, v), with d_sw != d."""
+    q, k, v = _inputs(1, 2, 9, 4, 3, seed=21)
+    q_sw, k_sw, _ = _inputs(1, 2, 9, 6, 3, seed=22)
+    want = ref.based_loops(q, k, v) + ref.sliding_loops(q_sw, k_sw, v, w)
+    got = ref.based_layer_dense(q, k, v, window_size=w, q_sw=q_sw, k_sw=k_sw)
+    assert np.abs(got.numpy() - want).max() < 1e-12
+    # the restated reference computes each branch as the reference does (fp32 inside for the
+    # softmax branch) and sums them
+    got32 = ref.ref_based_layer(q, k, v, window_size=w, q_sw=q_sw, k_sw=k_sw)
+    assert np.abs(got32.numpy() - want).max() < 1e-6
+    # default projections: both branches on q, k
+    want_same = ref.based_loops(q, k, v) + ref.sliding_loops(q, k, v, w)
+    assert np.abs(ref.based_layer_dense(q, k, v, window_size=w).numpy() - want_same).max() < 1e-12
+
+
 def test_sliding_banded_matches_dense():
     q, k, v = _inputs(1, 2, 300, 8, 4, seed=17)
     for w in (1, 13, 64, 300):

@@ -163,18 +163,22 @@ int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dty
   return la::launch_based_chunked(a, static_cast<hipStream_t>(hip_stream));
 }
 
-int la_sliding_window_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
-                          int H, int N, int d, int dv, int window, float scale, void* hip_stream) {
+static int sliding_common(const void* q, const void* k, const void* v, int in_dtype, bool with_addend,
+                          const float* addend, void* out, int out_dtype, int B, int H, int N, int d, int dv,
+                          int window, float scale, void* hip_stream) {
   int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
   if (rc != LA_OK) return rc;
   if (d > 128 || dv > 128) return LA_ERR_UNSUPPORTED_DIM;
   if (window < 1 || !finite_f(scale) || !(scale > 0.f)) return LA_ERR_BAD_SCALAR;
   if ((long long)B * H * N == 0) return LA_OK;
+  if (with_addend && addend == nullptr) return LA_ERR_NULL_POINTER;
+  if (with_addend && (reinterpret_cast<uintptr_t>(addend) & 15)) return LA_ERR_BAD_ALIGNMENT;
   la::SlidingArgs a{};
   a.q = q;
   a.k = k;
   a.v = v;
   a.out = out;
+  a.addend = addend;
   a.BH = B * H;
   a.N = N;
   a.d = d;
@@ -184,6 +188,18 @@ int la_sliding_window_fwd(const void* q, const void* k, const void* v, int in_dt
   a.in_f32 = in_dtype == LA_F32;
   a.out_f32 = out_dtype == LA_F32;
   return la::launch_sliding_window(a, static_cast<hipStream_t>(hip_stream));
+}
+
+int la_sliding_window_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
+                          int H, int N, int d, int dv, int window, float scale, void* hip_stream) {
+  return sliding_common(q, k, v, in_dtype, false, nullptr, out, out_dtype, B, H, N, d, dv, window, scale,
+                        hip_stream);
+}
+
+int la_sliding_window_fwd_add(const void* q, const void* k, const void* v, int in_dtype, const float* addend,
+                              void* out, int out_dtype, int B, int H, int N, int d, int dv, int window, float scale,
+                              void* hip_stream) {
+  return sliding_common(q, k, v, in_dtype, true, addend, out, out_dtype, B, H, N, d, dv, window, scale, hip_stream);
 }
 
 int la_taylor_feature_map(const void* x, int in_dtype, void* out, int out_dtype, long long rows, int d,

@@ -33,6 +33,7 @@ struct F32Params {
   const float* v;
   void* out;
   float* den;
+  const float* addend;   // sliding: optional fp32 addend of the output, or null
   int BH, N, d, dv, nqb, window;
   float inv_c, inv_c2, fscale, eps, scale_log2;
   int normalize, out_f32;
@@ -219,7 +220,8 @@ __global__ __launch_bounds__(256) void f32_attn_kernel(const F32Params p) {
     for (int i = 0; i < 16; ++i) {
       const int col = 32 * mt + c32_row(i, h);
       if (col < dv) {
-        const float y = acc[mt][i] * inv;
+        float y = acc[mt][i] * inv;
+        if (SLIDING && p.addend != nullptr) y += p.addend[obase + col];
         if (p.out_f32)
           static_cast<float*>(p.out)[obase + col] = y;
         else
@@ -279,6 +281,7 @@ int launch_sliding_window_f32(const SlidingArgs& a, hipStream_t stream) {
   p.k = static_cast<const float*>(a.k);
   p.v = static_cast<const float*>(a.v);
   p.out = a.out;
+  p.addend = a.addend;
   p.BH = a.BH;
   p.N = a.N;
   p.d = a.d;

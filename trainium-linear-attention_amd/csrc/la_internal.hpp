@@ -28,6 +28,7 @@ struct SlidingArgs {
   const void* k;
   const void* v;
   void* out;
+  const float* addend;   // optional fp32 (BH, N, dv) added to the output (may alias an fp32 out)
   int BH, N, d, dv, window;
   float scale;
   bool in_f32, out_f32;

@@ -127,9 +127,26 @@ __device__ __forceinline__ u32x4 load_row8(const uint16_t* __restrict__ rowp, in
   return x;
 }
 
-// Stores 4 consecutive output values of row `obase` starting at `col` (bounds-checked by dv).
+// Stores 4 consecutive output values of row `obase` starting at `col` (bounds-checked by dv),
+// plus the same elements of `addend` (fp32, same layout as the output) when it is not null.
+// Each element of addend is read by the thread that then writes it, so addend may be the output.
 template <bool VEC>
-__device__ __forceinline__ void store_out4(void* out, bool out_f32, size_t obase, int col, int dv, const float* y) {
+__device__ __forceinline__ void store_out4(void* out, bool out_f32, size_t obase, int col, int dv, const float* y_in,
+                                           const float* addend = nullptr) {
+  float y[4] = {y_in[0], y_in[1], y_in[2], y_in[3]};
+  if (addend != nullptr) {
+    if (VEC) {
+      if (col < dv) {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(addend + obase + col);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] += a[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (col + e < dv) y[e] += addend[obase + col + e];
+    }
+  }
   if (VEC) {
     if (col < dv) {
       if (out_f32)

@@ -28,6 +28,7 @@ struct SlidingParams {
   const uint16_t* k;
   const uint16_t* v;
   void* out;
+  const float* addend;   // optional fp32 addend of the output (16-byte aligned), or null
   int BH, N, d, dv, window, nqb;
   float scale_log2;   // scale * log2(e)
   int out_f32;
@@ -194,7 +195,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 8 ? 1
         float y[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) y[e] = acc[qt][mt][4 * g + e] * inv;
-        store_out4<VEC>(p.out, p.out_f32, obase, 32 * mt + 8 * g + 4 * h, dv, y);
+        store_out4<VEC>(p.out, p.out_f32, obase, 32 * mt + 8 * g + 4 * h, dv, y, p.addend);
       }
   }
 }
@@ -377,7 +378,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 8
           float y[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) y[e] = acc[mt][4 * g + e] * inv;
-          store_out4<true>(p.out, p.out_f32, obase, 32 * mt + 8 * g + 4 * h, DV, y);
+          store_out4<true>(p.out, p.out_f32, obase, 32 * mt + 8 * g + 4 * h, DV, y, p.addend);
         }
     }
   }
@@ -433,6 +434,7 @@ int launch_sliding_window(const SlidingArgs& a, hipStream_t stream) {
   p.k = static_cast<const uint16_t*>(a.k);
   p.v = static_cast<const uint16_t*>(a.v);
   p.out = a.out;
+  p.addend = a.addend;
   p.BH = a.BH;
   p.N = a.N;
   p.d = a.d;

@@ -45,10 +45,12 @@ _SIGNATURES = {
                                       _c_size, _c_void, _c_void]),
     "la_sliding_window_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
                                        _c_int, _c_int, _c_int, _c_int, _c_float, _c_void]),
+    "la_sliding_window_fwd_add": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int,
+                                           _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_void]),
     "la_taylor_feature_map": (_c_int, [_c_void, _c_int, _c_void, _c_int, ctypes.c_longlong, _c_int, _c_void]),
 }
 
-EXPECTED_ABI = 3
+EXPECTED_ABI = 4
 
 
 class BasedLAError(RuntimeError):
