@@ -65,6 +65,9 @@ def parse():
     ap.add_argument("--layer", action="store_true",
                     help="only time the full BASED layer (linear attention + sliding-window softmax, the sum "
                          "taken in the sliding kernel's store) against the two branches run and added apart")
+    ap.add_argument("--identity", action="store_true",
+                    help="only time the identity-map linear attention numerator (la_identity_linear_fwd) at "
+                         "B2 H16 N8192 d16 dv64 bf16 against its HBM roofline")
     ap.add_argument("--crossover", action="store_true",
                     help="only sweep sequence lengths: whole parallel forward vs chunked forward (d=16, dv=64, bf16), "
                          "the measurement behind solution()'s dispatch threshold")
@@ -271,6 +274,23 @@ def layer_bench(steps, warmup, device):
     return {"layer": rows}
 
 
+def identity_bench(steps, warmup, rotate, device):
+    """ms per call of the identity-map numerator; HBM-bound: algorithmic bytes = q, k, v read and
+    out written once (the per-block state records come on top)."""
+    import kernels as K
+
+    B, H, N, d, dv = 2, 16, 8192, 16, 64
+    sets = [make_inputs(B, H, N, d, dv, "bf16", 21 + r, True, device) for r in range(rotate)]
+    calls = [(lambda s=s: K.identity_linear_attn(*s)) for s in sets]
+    ms = time_calls(calls, steps, warmup)
+    nbytes = B * H * N * (2 * d + 2 * dv) * 2
+    flop = B * H * N * (4 * d * dv + 65 * (d + dv))   # Q S and state update, plus the causal 64-token block
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"identity": {"shape": {"B": B, "H": H, "N": N, "d": d, "dv": dv}, "ms": round(ms, 5),
+                         "gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "bytes": nbytes,
+                         "tflops": round(flop / (ms * 1e-3) / 1e12, 2), "input_sets": rotate}}
+
+
 def torch_empty_cache():
     import torch
 
@@ -332,6 +352,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": n * 4}))
+        return
+
+    if args.identity:
+        print(json.dumps(identity_bench(args.steps, args.warmup, args.rotate, device)))
         return
 
     if args.layer:

@@ -135,6 +135,23 @@ int la_sliding_window_fwd_add(const void* q, const void* k, const void* v, int i
                               int d, int dv, int window, float scale, void* hip_stream);
 
 /*
+ * Causal linear attention with the identity feature map, numerator only:
+ * out_t = sum_{u <= t} (scale q_t . k_u) v_u.
+ *
+ * Replaces ref_identity_numerator (benchmarks/chunked_attention_benchmark.py:81-93, scale
+ * 1/sqrt(d)) and the chunked identity NKI kernel (old/identity_linear_attn_nki_CHUNKED.py:27-59,
+ * whose state S = sum K^T V is carried here as exclusive prefixes over 64-token blocks).
+ * q, k: (B,H,N,d) bf16; v, out: (B,H,N,dv); q, k, v, out 16-byte aligned.
+ * workspace: device scratch of at least la_identity_workspace_bytes(...) bytes, 16-byte aligned.
+ * Limits: bf16 inputs, d in {16, 32, 64}, dv in {32, 64} (la_identity_workspace_bytes returns 0
+ * for other d, dv).
+ */
+size_t la_identity_workspace_bytes(int B, int H, int N, int d, int dv);
+int la_identity_linear_fwd(const void* q, const void* k, const void* v, int in_dtype,
+                           void* out, int out_dtype, int B, int H, int N, int d, int dv,
+                           float scale, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/*
  * BASED Taylor feature map, phi(x) = [1, x/d^(1/4), x_i^2/(sqrt(d) sqrt(2)),
  * x_i x_j/sqrt(d) (i<j, row-major upper-triangle order)], rows x (rows, d) -> (rows, F).
  *

@@ -27,7 +27,8 @@ def test_header_declares_expected_entry_points():
     assert _declared() == sorted([
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
         "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_fwd", "la_sliding_window_fwd",
-        "la_sliding_window_fwd_add", "la_taylor_feature_map"])
+        "la_sliding_window_fwd_add", "la_identity_workspace_bytes", "la_identity_linear_fwd",
+        "la_taylor_feature_map"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -98,6 +99,33 @@ def test_sliding_add_argument_errors():
     assert call(12, 0) == -4                       # window
     assert call(10, 129) == -5                     # d
     assert call(9, 0) == 0                         # N = 0: nothing to launch
+
+
+def test_identity_workspace_and_argument_errors():
+    lib = _lib()
+    ws = lib.la_identity_workspace_bytes
+    # one fp32 (dv x d) record per 64-token block of every head
+    assert ws(2, 16, 8192, 16, 64) == 32 * 128 * 64 * 16 * 4
+    assert ws(1, 1, 65, 64, 32) == 2 * 32 * 64 * 4
+    assert ws(1, 1, 64, 48, 64) == 0 and ws(1, 1, 64, 16, 16) == 0   # outside the kernel's d, dv
+    f = lib.la_identity_linear_fwd
+    need = ws(1, 1, 8, 16, 64)
+    ok = [P, P, P, 1, P, 1, 1, 1, 8, 16, 64, 0.25, P, need, None]
+
+    def call(i, x):
+        a = list(ok)
+        a[i] = x
+        return f(*a)
+
+    assert call(0, None) == -1
+    assert call(3, 0) == -3                              # fp32 inputs
+    assert call(9, 48) == -5                             # d
+    assert call(10, 16) == -5                            # dv
+    assert call(11, float("inf")) == -4
+    assert call(4, ctypes.c_void_p(24)) == -8            # out not 16-byte aligned
+    assert call(12, None) == -6
+    assert call(13, need - 1) == -6
+    assert call(8, 0) == 0                               # N = 0
 
 
 def test_parallel_pack_and_packed_argument_errors():

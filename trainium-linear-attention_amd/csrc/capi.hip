@@ -163,6 +163,42 @@ int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dty
   return la::launch_based_chunked(a, static_cast<hipStream_t>(hip_stream));
 }
 
+size_t la_identity_workspace_bytes(int B, int H, int N, int d, int dv) {
+  if (B < 0 || H < 0 || N < 0) return 0;
+  return la::identity_workspace_bytes(B * H, N, d, dv);
+}
+
+int la_identity_linear_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
+                           int H, int N, int d, int dv, float scale, void* workspace, size_t workspace_bytes,
+                           void* hip_stream) {
+  int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
+  if (rc != LA_OK) return rc;
+  if (in_dtype != LA_BF16) return LA_ERR_BAD_DTYPE;
+  if (!la::identity_shape(d, dv)) return LA_ERR_UNSUPPORTED_DIM;
+  if (!finite_f(scale)) return LA_ERR_BAD_SCALAR;
+  if ((long long)B * H * N == 0) return LA_OK;
+  if ((size_t)N * (size_t)(d > dv ? d : dv) * 2 >= ((size_t)1 << 31)) return LA_ERR_BAD_SHAPE;
+  if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+        reinterpret_cast<uintptr_t>(out)) & 15) != 0)
+    return LA_ERR_BAD_ALIGNMENT;
+  const size_t need = la::identity_workspace_bytes(B * H, N, d, dv);
+  if (workspace == nullptr || workspace_bytes < need) return LA_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(workspace) & 15) return LA_ERR_BAD_ALIGNMENT;
+  la::IdentityArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.workspace = workspace;
+  a.BH = B * H;
+  a.N = N;
+  a.d = d;
+  a.dv = dv;
+  a.scale = scale;
+  a.out_f32 = out_dtype == LA_F32;
+  return la::launch_identity(a, static_cast<hipStream_t>(hip_stream));
+}
+
 static int sliding_common(const void* q, const void* k, const void* v, int in_dtype, bool with_addend,
                           const float* addend, void* out, int out_dtype, int B, int H, int N, int d, int dv,
                           int window, float scale, void* hip_stream) {

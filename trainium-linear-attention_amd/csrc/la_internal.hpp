@@ -48,6 +48,17 @@ struct ChunkedArgs {
   bool in_f32, out_f32;
 };
 
+struct IdentityArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  void* workspace;     // identity_workspace_bytes() bytes, 16-byte aligned
+  int BH, N, d, dv;
+  float scale;
+  bool out_f32;
+};
+
 struct FeatureMapArgs {
   const void* x;
   void* out;
@@ -64,6 +75,9 @@ int launch_sliding_window(const SlidingArgs& a, hipStream_t stream);
 size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk);
 int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream);
 int launch_feature_map(const FeatureMapArgs& a, hipStream_t stream);
+bool identity_shape(int d, int dv);
+size_t identity_workspace_bytes(int BH, int N, int d, int dv);
+int launch_identity(const IdentityArgs& a, hipStream_t stream);
 
 // Work-group order for causal query blocks: heaviest (last) blocks first over all the heads an
 // XCD owns, so that greedy dispatch as slots free up balances the causal triangle (a head-major

@@ -47,6 +47,9 @@ _SIGNATURES = {
                                        _c_int, _c_int, _c_int, _c_int, _c_float, _c_void]),
     "la_sliding_window_fwd_add": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int,
                                            _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_void]),
+    "la_identity_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "la_identity_linear_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int, _c_int,
+                                        _c_int, _c_int, _c_float, _c_void, _c_size, _c_void]),
     "la_taylor_feature_map": (_c_int, [_c_void, _c_int, _c_void, _c_int, ctypes.c_longlong, _c_int, _c_void]),
 }
 
