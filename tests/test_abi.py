@@ -104,9 +104,9 @@ def test_sliding_add_argument_errors():
 def test_identity_workspace_and_argument_errors():
     lib = _lib()
     ws = lib.la_identity_workspace_bytes
-    # one fp32 (dv x d) record per 64-token block of every head
-    assert ws(2, 16, 8192, 16, 64) == 32 * 128 * 64 * 16 * 4
-    assert ws(1, 1, 65, 64, 32) == 2 * 32 * 64 * 4
+    # one fp32 (dv x d) record per 256-token span of every head
+    assert ws(2, 16, 8192, 16, 64) == 32 * 32 * 64 * 16 * 4
+    assert ws(1, 1, 257, 64, 32) == 2 * 32 * 64 * 4
     assert ws(1, 1, 64, 48, 64) == 0 and ws(1, 1, 64, 16, 16) == 0   # outside the kernel's d, dv
     f = lib.la_identity_linear_fwd
     need = ws(1, 1, 8, 16, 64)

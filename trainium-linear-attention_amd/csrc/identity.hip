@@ -3,19 +3,21 @@
 // the reference's ref_identity_numerator (benchmarks/chunked_attention_benchmark.py:81-93) and
 // its chunked NKI form (old/identity_linear_attn_nki_CHUNKED.py:27-59: inter-chunk Q S, masked
 // intra-chunk (Q K^T) V, state S += K^T V), evaluated sequence-parallel in three passes over
-// 64-token blocks:
-//  1. identity_kernel<STATE = true>: the increment of every block, dS^T = V_b^T K_b (dv x d,
-//     fp32), written to a workspace record per block;
-//  2. stats_scan_kernel: exclusive prefix of the records over the blocks of a head, in place;
-//  3. identity_kernel<STATE = false>: per 32-query wave, O^T = S^T_{<b} Q^T (S^T split into bf16
-//     hi + lo) + V_b^T P^T with P = mask(K_b Q^T) of its 64-token diagonal block (P split into
-//     bf16 hi + lo), times scale at the store.
-// A work-group (8 waves) covers 4 blocks: their K and V rows are copied global -> LDS once
-// with buffer_load ... lds (16-byte chunks XOR-swizzled by row), then the waves run without
-// synchronisation.  Operand layouts as in the resident sliding-window kernel: K fragments are
-// ds_read_b128; V^T fragments, and in pass 1 the K^T-ordered B operand, come from the
-// row-major rows through ds_read_b64_tr_b16 (in a 16-lane group, lane i receives element i % 4
-// of the 8-byte chunk read by lane 4 r + i / 4 as its element r).
+// 256-token spans (4 blocks of 64 tokens, one work-group of 8 waves each):
+//  1. identity_kernel<STATE = true>: the increment of every span, dS^T = V^T K over its 256 keys
+//     (dv x d, fp32), written to a workspace record per span;
+//  2. stats_scan_kernel: exclusive prefix of the records over the spans of a head, in place;
+//  3. identity_kernel<STATE = false>: per 32-query wave in block b of a span, O^T = S^T Q^T with
+//     S = the record (keys before the span) + K^T V over the span's blocks before b (an MFMA
+//     product from LDS whose accumulator rows are already the A operand of S^T Q^T under a fixed
+//     permutation of d, which Q^T takes on when it is loaded), split into bf16 hi + lo; plus
+//     V_b^T P^T with P = mask(K_b Q^T) of the diagonal block (hi + lo); times scale at the store.
+// Each pass copies the span's K and V rows global -> LDS once with buffer_load ... lds (16-byte
+// chunks XOR-swizzled by row); the waves then run without synchronisation.  Operand layouts as
+// in the resident sliding-window kernel: K fragments are ds_read_b128; V^T fragments, and in
+// pass 1 the K^T-ordered B operand, come from the row-major rows through ds_read_b64_tr_b16 (in
+// a 16-lane group, lane i receives element i % 4 of the 8-byte chunk read by lane 4 r + i / 4 as
+// its element r).
 #include "la_common.hpp"
 #include "la_internal.hpp"
 #include "la_pack.hpp"
@@ -30,8 +32,8 @@ struct IdentityParams {
   const uint16_t* k;
   const uint16_t* v;
   void* out;
-  float* state;     // [BH][nb][DV * DK] fp32: block increments, then their exclusive prefixes
-  int BH, N, nb;    // nb = number of 64-token blocks
+  float* state;     // [BH][ns][DV * DK] fp32: span increments, then their exclusive prefixes
+  int BH, N, nb, ns;   // 64-token blocks and 256-token spans per head
   float scale;
   int out_f32;
 };
@@ -43,7 +45,8 @@ __device__ __forceinline__ int id_swz_k(int row, int nch) { return row % nch; }
 __device__ __forceinline__ int id_swz_v(int row, int nch) { return (row >> 1) % nch; }
 
 template <int KS, int MT, bool STATE>
-__global__ __launch_bounds__(64 * kIdNW) void identity_kernel(const IdentityParams p) {
+__global__ __launch_bounds__(64 * kIdNW) __attribute__((amdgpu_waves_per_eu(KS * MT <= 2 ? 6 : 2))) void identity_kernel(
+    const IdentityParams p) {
   constexpr int NW = kIdNW, NBK = kIdBlocks, DK = 16 * KS, DV = 32 * MT;
   constexpr int KCH = DK / 8, VCH = DV / 8;
   constexpr int KU = BN * DK * 2 / 1024, VU = BN * DV * 2 / 1024;   // 1 KB copy units per block
@@ -99,14 +102,14 @@ __global__ __launch_bounds__(64 * kIdNW) void identity_kernel(const IdentityPara
     __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's copies landed
     __builtin_amdgcn_s_barrier();          // every wave's copies landed
     asm volatile("" ::: "memory");
-    // wave w: block w / 2, dv tile w % 2 (waves with an odd index idle when MT == 1)
-    const int b = w >> 1, mt = w & 1;
-    if (b >= nbk || mt >= MT) return;
+    // wave w < MT * NC: dv tile w % MT, d tile w / MT, over the keys of all blocks of the span
     constexpr int NC = (DK + 31) / 32;   // 32-wide column tiles of d
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
+    const int mt = w % MT, c = w / MT;
+    if (c >= NC) return;
+    {
       f32x16 acc = splat16(0.f);
       const bool colok = 32 * c + 16 * gh < DK;   // whole 16-lane groups are in or out of range
+      for (int b = 0; b < nbk; ++b)
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         // keys 16 m + 8 s2 + 4 h + 0..3 for element 4 s2 + 0..3, in A (V^T) and B (K) alike
@@ -124,7 +127,7 @@ __global__ __launch_bounds__(64 * kIdNW) void identity_kernel(const IdentityPara
         acc = mfma32x32x16((u32x4){va[0], va[1], va[2], va[3]}, (u32x4){kb[0], kb[1], kb[2], kb[3]}, acc);
       }
       // acc: lane column d = 32 c + n, rows dv = 32 mt + c32_row(i, h)
-      float* rec = p.state + ((size_t)bh * p.nb + b0 + b) * SW;
+      float* rec = p.state + ((size_t)bh * p.ns + blockIdx.x) * SW;
       if (32 * c + n < DK) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) rec[(32 * mt + c32_row(i, h)) * DK + 32 * c + n] = acc[i];
@@ -137,62 +140,98 @@ __global__ __launch_bounds__(64 * kIdNW) void identity_kernel(const IdentityPara
   const int bq = w >> 1;
   const int wq0 = (b0 * BN) + 32 * w;
   const bool wave_live = bq < nbk && wq0 < N;
-  const uint16_t* __restrict__ qg = p.q + hrow * DK;
-  u32x4 qf[KS];
+  const bool qok = wave_live && wq0 + n < N;
+  const uint16_t* __restrict__ qrow = p.q + hrow * DK + (size_t)(wq0 + n) * DK;
+  // Q^T as the B operand: qf in natural order (k = 16 kk + 8 h + e, for the scores against the
+  // K rows), qp in the order of the state accumulator rows (k = 16 kk + 8 (e / 4) + 4 h + e % 4)
+  u32x4 qf[KS], qp[KS];
 #pragma unroll
-  for (int kk = 0; kk < KS; ++kk) qf[kk] = load_row8<true>(qg + (size_t)(wq0 + n) * DK, 16 * kk + 8 * h, DK, wave_live && wq0 + n < N);
-  // S^T prefix of this wave's block as A fragments (rows dv, k = d), split into bf16 hi + lo
-  u32x4 shi[MT][KS], slo[MT][KS];
-  {
-    const float* rec = p.state + ((size_t)bh * p.nb + (wave_live ? b0 + bq : 0)) * SW;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        const float* src = rec + (32 * mt + n) * DK + 16 * kk + 8 * h;
-        f32x4 a = {0.f, 0.f, 0.f, 0.f}, bb = {0.f, 0.f, 0.f, 0.f};
-        if (wave_live) {
-          a = *reinterpret_cast<const f32x4*>(src);
-          bb = *reinterpret_cast<const f32x4*>(src + 4);
-        }
-        const float x[8] = {a[0], a[1], a[2], a[3], bb[0], bb[1], bb[2], bb[3]};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const u32 hi = pack_bf16x2(x[2 * c], x[2 * c + 1]);
-          shi[mt][kk][c] = hi;
-          slo[mt][kk][c] = pack_bf16x2(x[2 * c] - bf16_lo_to_f32(hi), x[2 * c + 1] - bf16_hi_to_f32(hi));
-        }
-      }
+  for (int kk = 0; kk < KS; ++kk) {
+    qf[kk] = load_row8<true>(qrow, 16 * kk + 8 * h, DK, qok);
+    u32x2 lo = {0u, 0u}, hi = {0u, 0u};
+    if (qok) {
+      lo = *reinterpret_cast<const u32x2*>(qrow + 16 * kk + 4 * h);
+      hi = *reinterpret_cast<const u32x2*>(qrow + 16 * kk + 8 + 4 * h);
+    }
+    qp[kk] = (u32x4){lo[0], lo[1], hi[0], hi[1]};
   }
-
   asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's copies, Q rows and state landed
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): this wave's copies and Q rows landed
   __builtin_amdgcn_s_barrier();          // every wave's copies landed
   asm volatile("" ::: "memory");
   if (!wave_live) return;
 
+  // O^T = S^T Q^T, one (dv tile mt, d tile c) of S at a time.  S (rows d, columns dv) starts as
+  // the span's record (S^T before the span, [dv][d] fp32) in the MFMA accumulator layout (lane
+  // column dv = 32 mt + n, rows d = 32 c + 8 g + 4 h + 0..3 for elements 4 g .. 4 g + 3), then
+  // S += K^T V over the span's blocks before bq (MFMA A = K^T and B = V, both transposed reads
+  // from the row-major blocks, keys in the same order).  For K step kk = 2 c + kk2 the lane's A
+  // values are elements 8 kk2 .. 8 kk2 + 7 (rows d = 16 kk + 8 (e / 4) + 4 h + e % 4, the order
+  // of qp), split into bf16 hi + lo.
+  constexpr int NC = (DK + 31) / 32;
+  const float* rec = p.state + ((size_t)bh * p.ns + blockIdx.x) * SW;
   f32x16 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     acc[mt] = splat16(0.f);
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
-      acc[mt] = mfma32x32x16(shi[mt][kk], qf[kk], acc[mt]);
-      acc[mt] = mfma32x32x16(slo[mt][kk], qf[kk], acc[mt]);
+    for (int c = 0; c < NC; ++c) {
+      f32x16 st;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 32 * c + 8 * g + 4 * h;
+        f32x4 x = {0.f, 0.f, 0.f, 0.f};
+        if (d0 < DK) x = *reinterpret_cast<const f32x4*>(rec + (32 * mt + n) * DK + d0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st[4 * g + e] = x[e];
+      }
+      const bool colok = 32 * c + 16 * gh < DK;
+      for (int jb = 0; jb < bq; ++jb)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          u32 ka[4], vb[4];
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            const int row = 16 * m + 8 * s2 + 4 * h + (gi >> 2);
+            const u32x2 kk2 = tr_read(&Kl[jb][0], DK, KCH, false, row, colok ? 32 * c + 16 * gh + 4 * (gi & 3) : 0);
+            const u32x2 vv = tr_read(&Vl[jb][0], DV, VCH, true, row, 32 * mt + 16 * gh + 4 * (gi & 3));
+            ka[2 * s2] = colok ? kk2[0] : 0u;
+            ka[2 * s2 + 1] = colok ? kk2[1] : 0u;
+            vb[2 * s2] = vv[0];
+            vb[2 * s2 + 1] = vv[1];
+          }
+          st = mfma32x32x16((u32x4){ka[0], ka[1], ka[2], ka[3]}, (u32x4){vb[0], vb[1], vb[2], vb[3]}, st);
+        }
+#pragma unroll
+      for (int kk2 = 0; kk2 < 2; ++kk2) {
+        const int kk = 2 * c + kk2;
+        if (kk >= KS) break;
+        u32 hi[4], lo[4];
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const float x0 = st[8 * kk2 + 2 * e2], x1 = st[8 * kk2 + 2 * e2 + 1];
+          const u32 ph = pack_bf16x2(x0, x1);
+          hi[e2] = ph;
+          lo[e2] = pack_bf16x2(x0 - bf16_lo_to_f32(ph), x1 - bf16_hi_to_f32(ph));
+        }
+        acc[mt] = mfma32x32x16((u32x4){hi[0], hi[1], hi[2], hi[3]}, qp[kk], acc[mt]);
+        acc[mt] = mfma32x32x16((u32x4){lo[0], lo[1], lo[2], lo[3]}, qp[kk], acc[mt]);
+      }
     }
   }
 
-  // diagonal block: keys bq * 64 + 32 ks + 0..31 up to the wave's last query
+  // diagonal block bq: keys up to the wave's last query, 32-key halves ks, causal mask
   const int query = wq0 + n;
+  const int jb = bq;
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
-    const int kb = (b0 + bq) * BN + 32 * ks;
+    const int kb = (b0 + jb) * BN + 32 * ks;
     if (kb > wq0 + 31) continue;
     u32x4 kf[KS];
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       const int row = 32 * ks + n, c = 2 * kk + h;
-      kf[kk] = *reinterpret_cast<const u32x4*>(&Kl[bq][row * DK + 8 * (c ^ id_swz_k(row, KCH))]);
+      kf[kk] = *reinterpret_cast<const u32x4*>(&Kl[jb][row * DK + 8 * (c ^ id_swz_k(row, KCH))]);
     }
     f32x16 sc = splat16(0.f);
 #pragma unroll
@@ -223,7 +262,7 @@ __global__ __launch_bounds__(64 * kIdNW) void identity_kernel(const IdentityPara
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           const int row = 32 * ks + 16 * m + 8 * s2 + 4 * h + (gi >> 2);
-          const u32x2 r2 = tr_read(&Vl[bq][0], DV, VCH, true, row, 32 * mt + 16 * gh + 4 * (gi & 3));
+          const u32x2 r2 = tr_read(&Vl[jb][0], DV, VCH, true, row, 32 * mt + 16 * gh + 4 * (gi & 3));
           vv[2 * s2] = r2[0];
           vv[2 * s2 + 1] = r2[1];
         }
@@ -251,10 +290,10 @@ __global__ __launch_bounds__(64 * kIdNW) void identity_kernel(const IdentityPara
 
 template <int KS, int MT>
 int launch_identity_t(IdentityParams p, hipStream_t stream) {
-  const dim3 grid((unsigned)((p.nb + kIdBlocks - 1) / kIdBlocks), (unsigned)p.BH), block(64 * kIdNW);
+  const dim3 grid((unsigned)p.ns, (unsigned)p.BH), block(64 * kIdNW);
   hipLaunchKernelGGL((identity_kernel<KS, MT, true>), grid, block, 0, stream, p);
   hipLaunchKernelGGL(stats_scan_kernel, dim3((unsigned)p.BH, (unsigned)(32 * MT * 16 * KS / 16)), dim3(256), 0, stream,
-                     p.state, p.nb, 32 * MT * 16 * KS);
+                     p.state, p.ns, 32 * MT * 16 * KS);
   hipLaunchKernelGGL((identity_kernel<KS, MT, false>), grid, block, 0, stream, p);
   return (int)hipGetLastError();
 }
@@ -265,7 +304,7 @@ bool identity_shape(int d, int dv) { return (d == 16 || d == 32 || d == 64) && (
 
 size_t identity_workspace_bytes(int BH, int N, int d, int dv) {
   if (!identity_shape(d, dv)) return 0;
-  return (size_t)BH * (((size_t)N + BN - 1) / BN) * (size_t)d * (size_t)dv * 4;
+  return (size_t)BH * (((size_t)N + kIdBlocks * BN - 1) / (kIdBlocks * BN)) * (size_t)d * (size_t)dv * 4;
 }
 
 int launch_identity(const IdentityArgs& a, hipStream_t stream) {
@@ -278,6 +317,7 @@ int launch_identity(const IdentityArgs& a, hipStream_t stream) {
   p.BH = a.BH;
   p.N = a.N;
   p.nb = (a.N + BN - 1) / BN;
+  p.ns = (p.nb + kIdBlocks - 1) / kIdBlocks;
   p.scale = a.scale;
   p.out_f32 = a.out_f32 ? 1 : 0;
   const int ks = a.d / 16;
