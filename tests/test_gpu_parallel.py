@@ -224,3 +224,17 @@ def test_solution_dispatch_by_length(N, d, dv, dtype):
         assert rounded_err(y, want) < TOL_BF16     # bf16 output
     else:
         assert err(y, want) < TOL_F32
+
+
+@pytest.mark.parametrize("B,H,N,dv", [(8, 32, 300, 64), (8, 32, 600, 32), (8, 32, 257, 32), (1, 2, 777, 64),
+                                      (1, 3, 129, 32)])
+def test_packed_work_group_sizes(B, H, N, dv):
+    """The packed kernel runs 256-query work-groups when they fill every CU's slots (two per CU
+    at dv = 64, three at dv = 32: the first two shapes at 256 CUs) and 128-query ones below that;
+    ragged N in both."""
+    K = _kernels()
+    q, k, v = rand_qkv(B, H, N, 16, dv, seed=N + dv + H, dtype=torch.bfloat16, scale_qk=0.5)
+    y, den = K.based_parallel(*to_dev(q, k, v), out_dtype=torch.float32, return_den=True)
+    want, _, want_den = ref.based_dense(q, k, v)
+    assert err(y, want) < TOL_BF16
+    assert err(den, want_den) < TOL_BF16

@@ -608,7 +608,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
 
   const float fscale = p.fscale;
   if (PACKED) {
-    // The wave's output tile (64 queries x DV) goes through its own part of the free stages so
+    // The wave's output tile (32 QT queries x DV) goes through its own part of the free stages so
     // that the stores write whole rows: lane -> (row, 16-byte chunk).
     auto store_tile = [&](auto f32_tag) {
       constexpr bool F32 = decltype(f32_tag)::value;
@@ -639,7 +639,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       const int rowbytes = dv * EB;
       char* out = static_cast<char*>(p.out) + (hrow + wq0) * (size_t)rowbytes;
 #pragma unroll
-      for (int it = 0; it < CPR; ++it) {
+      for (int it = 0; it < CPR * QT / 2; ++it) {   // the wave's 32 QT rows, no more
         const int idx = 64 * it + lane, r = idx / CPR, c = idx % CPR;
         const u32x4 x = *reinterpret_cast<const u32x4*>(tile + r * RS + 16 * c);
         if (wq0 + r < N && 16 * c < rowbytes) *reinterpret_cast<u32x4*>(out + (size_t)r * rowbytes + 16 * c) = x;
@@ -693,11 +693,24 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   }
 }
 
-// Packed path: pre-pass, column-sum scan, then the main kernel with 4 waves x 64 queries (8 waves
-// x 32 queries at four waves per SIMD measured slower).
-template <int MT>
+// Compute units of the current device (256 on MI355X when the query fails).
+int device_cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Packed path: pre-pass, column-sum scan, then the main kernel with 4 waves x 32 QT queries (8
+// waves x 32 queries at four waves per SIMD measured slower).
+template <int MT, int QT>
 int launch_packed(const ParallelParams& pp, int stages, hipStream_t stream) {
-  constexpr int DV = 32 * MT, QT = 2, NW = 4, BM = 32 * QT * NW;
+  constexpr int DV = 32 * MT, NW = 4, BM = 32 * QT * NW;
   ParallelParams p = pp;
   p.nqb = (p.N + BM - 1) / BM;
   if (stages & 1) {
@@ -722,7 +735,14 @@ int launch_packed(const ParallelParams& pp, int stages, hipStream_t stream) {
 template <int KS, int MT, int QT>
 int launch_bf16(const ParallelParams& pp, bool vec, bool packed, int stages, hipStream_t stream) {
   if constexpr (KS == 1 && MT <= 2) {
-    if (packed) return launch_packed<MT>(pp, stages, stream);
+    // 256-query work-groups once they fill every CU's slots, else 128-query ones (twice as many,
+    // the longest one half as long).  Slots per CU: two (LDS, registers); at dv <= 32 the
+    // 128-query kernel fits three, and measured faster up to 2-3 256-query work-groups per CU.
+    if (packed) {
+      const long long wg256 = (long long)((pp.N + 255) / 256) * pp.BH;
+      return wg256 >= (MT == 1 ? 3LL : 2LL) * device_cu_count() ? launch_packed<MT, 2>(pp, stages, stream)
+                                                                 : launch_packed<MT, 1>(pp, stages, stream);
+    }
   }
   if (!(stages & 2)) return 0;
   constexpr int BM = 128 * QT;
