@@ -66,6 +66,8 @@ def parse():
     ap.add_argument("--layer", action="store_true",
                     help="only time the full BASED layer (linear attention + sliding-window softmax, the sum "
                          "taken in the sliding kernel's store) against the two branches run and added apart")
+    ap.add_argument("--decode", action="store_true",
+                    help="only time one decode step (la_based_decode_step, d16 dv64) on the exported state")
     ap.add_argument("--identity", action="store_true",
                     help="only time the identity-map linear attention numerator (la_identity_linear_fwd) at "
                          "B2 H16 N8192 d16 dv64 bf16 against its HBM roofline")
@@ -275,6 +277,43 @@ def layer_bench(steps, warmup, device):
     return {"layer": rows}
 
 
+def _lib_handle():
+    from kernels import _lib
+
+    return _lib.lib()
+
+
+def decode_bench(steps, warmup, device):
+    """ms per decode step (one token per head) at a serving batch and at the headline's heads;
+    HBM-bound: the fp32 state is read and written once, 2 x 4 F (dv + 1) bytes per head."""
+    import torch
+
+    import kernels as K
+
+    rows = []
+    for B, H in [(2, 16), (64, 16)]:
+        d, dv, F = 16, 64, K.feature_dim(16)
+        g = torch.Generator(device=device).manual_seed(3)
+        q, k, v = (torch.randn(B, H, n, generator=g, device=device).bfloat16() * 0.5 for n in (d, d, dv))
+        st = torch.zeros(B, H, F, dv + 1, device=device)
+        out = torch.empty(B, H, dv, dtype=torch.bfloat16, device=device)
+        L = _lib_handle()
+        stream = torch.cuda.current_stream(device).cuda_stream
+
+        def abi():
+            rc = L.la_based_decode_step(q.data_ptr(), k.data_ptr(), v.data_ptr(), 1, st.data_ptr(), out.data_ptr(), 1,
+                                        B, H, d, dv, 1e-6, 1, stream)
+            if rc != 0:
+                raise RuntimeError(f"la_based_decode_step: {rc}")
+
+        ms = time_calls([abi], steps, warmup)
+        ms_py = time_calls([lambda: K.based_decode_step(q, k, v, st)], steps, warmup)
+        nbytes = 2 * B * H * F * (dv + 1) * 4
+        rows.append({"B": B, "H": H, "d": d, "dv": dv, "ms": round(ms, 5), "ms_python_wrapper": round(ms_py, 5),
+                     "state_bytes_moved": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+    return {"decode": rows}
+
+
 def identity_bench(steps, warmup, rotate, device):
     """ms per call of the identity-map numerator; HBM-bound: algorithmic bytes = q, k, v read and
     out written once (the per-block state records come on top)."""
@@ -362,6 +401,10 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": n * 4}))
+        return
+
+    if args.decode:
+        print(json.dumps(decode_bench(args.steps, args.warmup, device)))
         return
 
     if args.identity:

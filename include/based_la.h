@@ -135,6 +135,20 @@ int la_sliding_window_fwd_add(const void* q, const void* k, const void* v, int i
                               int d, int dv, int window, float scale, void* hip_stream);
 
 /*
+ * One decode step of BASED attention on an exported state (no reference counterpart: the
+ * reference has no decode path; this continues la_based_chunked_fwd's state_out).
+ * state: fp32 (B,H,F,dv+1), F = 1 + d + d(d+1)/2, [S | z] in the feature order of
+ * taylor_feature_map (benchmarks/chunked_attention_benchmark.py:34-53), updated in place with the
+ * new token: [S | z] += phi(k) [v | 1].  Then out = phi(q)^T S / (phi(q)^T z + eps) with
+ * normalize = 1 (the numerator phi(q)^T S with normalize = 0), which is the chunk recurrence of
+ * kernels/nki_attention_chunked.py:65-109 for a chunk of one token.
+ * q, k: (B,H,d) (one token per head); v, out: (B,H,dv).  Limits: 1 <= d <= 64, 1 <= dv <= 128.
+ */
+int la_based_decode_step(const void* q, const void* k, const void* v, int in_dtype,
+                         float* state, void* out, int out_dtype, int B, int H, int d, int dv,
+                         float eps, int normalize, void* hip_stream);
+
+/*
  * Causal linear attention with the identity feature map, numerator only:
  * out_t = sum_{u <= t} (scale q_t . k_u) v_u.
  *

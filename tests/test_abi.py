@@ -27,7 +27,7 @@ def test_header_declares_expected_entry_points():
     assert _declared() == sorted([
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
         "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_fwd", "la_sliding_window_fwd",
-        "la_sliding_window_fwd_add", "la_identity_workspace_bytes", "la_identity_linear_fwd",
+        "la_sliding_window_fwd_add", "la_based_decode_step", "la_identity_workspace_bytes", "la_identity_linear_fwd",
         "la_taylor_feature_map"])
 
 
@@ -99,6 +99,25 @@ def test_sliding_add_argument_errors():
     assert call(12, 0) == -4                       # window
     assert call(10, 129) == -5                     # d
     assert call(9, 0) == 0                         # N = 0: nothing to launch
+
+
+def test_decode_argument_errors():
+    lib = _lib()
+    f = lib.la_based_decode_step
+    ok = [P, P, P, 1, P, P, 1, 1, 2, 16, 64, 1e-6, 1, None]
+
+    def call(i, x):
+        a = list(ok)
+        a[i] = x
+        return f(*a)
+
+    assert call(4, None) == -1                        # state
+    assert call(4, ctypes.c_void_p(18)) == -8         # state not 4-byte aligned
+    assert call(9, 65) == -5                          # d
+    assert call(10, 129) == -5                        # dv
+    assert call(11, -1.0) == -4                       # eps
+    assert call(3, 5) == -3                           # dtype
+    assert call(7, 0) == 0                            # B = 0: nothing to launch
 
 
 def test_identity_workspace_and_argument_errors():

@@ -199,6 +199,31 @@ int la_identity_linear_fwd(const void* q, const void* k, const void* v, int in_d
   return la::launch_identity(a, static_cast<hipStream_t>(hip_stream));
 }
 
+int la_based_decode_step(const void* q, const void* k, const void* v, int in_dtype, float* state, void* out,
+                         int out_dtype, int B, int H, int d, int dv, float eps, int normalize, void* hip_stream) {
+  int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, 1, d, dv);
+  if (rc != LA_OK) return rc;
+  if (!la::decode_shape(d, dv)) return LA_ERR_UNSUPPORTED_DIM;
+  if (!finite_f(eps) || eps < 0.f) return LA_ERR_BAD_SCALAR;
+  if ((long long)B * H == 0) return LA_OK;
+  if (state == nullptr) return LA_ERR_NULL_POINTER;
+  if (reinterpret_cast<uintptr_t>(state) & 3) return LA_ERR_BAD_ALIGNMENT;
+  la::DecodeArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.state = state;
+  a.out = out;
+  a.BH = B * H;
+  a.d = d;
+  a.dv = dv;
+  a.eps = eps;
+  a.normalize = normalize != 0;
+  a.in_f32 = in_dtype == LA_F32;
+  a.out_f32 = out_dtype == LA_F32;
+  return la::launch_decode_step(a, static_cast<hipStream_t>(hip_stream));
+}
+
 static int sliding_common(const void* q, const void* k, const void* v, int in_dtype, bool with_addend,
                           const float* addend, void* out, int out_dtype, int B, int H, int N, int d, int dv,
                           int window, float scale, void* hip_stream) {

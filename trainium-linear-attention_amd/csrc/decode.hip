@@ -1,0 +1,138 @@
+// One recurrent (decode) step of BASED causal linear attention for gfx950, on the state the
+// chunked kernel exports: per head the fp32 (F x (dv + 1)) matrix [S | z] with
+// S = sum_u phi(k_u) v_u^T and z = sum_u phi(k_u) over the tokens so far, phi the Taylor
+// feature map of benchmarks/chunked_attention_benchmark.py:34-53 in its order
+//   phi(x) = [1, x_i / d^(1/4), x_i^2 / (sqrt(d) sqrt(2)), x_i x_j / sqrt(d) (i < j, row-major)],
+// F = 1 + d + d(d+1)/2, so that phi(q).phi(k) = 1 + s + s^2/2 with s = q.k / sqrt(d).
+// For the new token (q, k, v) of every head the step does
+//   [S | z] += phi(k) [v | 1],   num = phi(q)^T [S | z],   y = num[:dv] / (num[dv] + eps)
+// which is the chunk recurrence of kernels/nki_attention_chunked.py:65-109 for a chunk of one
+// token (its intra-chunk term phi(q).phi(k) v is the contribution of the token's own row of the
+// update).  The reference has no decode path; this continues a prefill that exported its state.
+//
+// One work-group per head: phi(q) and phi(k) go to LDS, then the head's state is swept linearly
+// (coalesced) in tiles of 32 rows, each element updated in place, and the column sums of phi(q)
+// times the updated state are taken per tile through LDS in row order (deterministic).
+// HBM-bound: the state is read and written once (4 F (dv + 1) bytes each way per head).
+#include <math.h>
+
+#include "la_common.hpp"
+#include "la_internal.hpp"
+
+namespace la {
+
+namespace {
+
+struct DecodeParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  float* state;
+  void* out;
+  int BH, d, dv, F;
+  float eps;
+  int normalize, in_f32, out_f32;
+};
+
+constexpr int kDecThreads = 256;
+constexpr int kDecMaxD = 64;
+constexpr int kDecMaxC = 129;   // dv + 1 for dv <= 128
+constexpr int kDecMaxF = 1 + kDecMaxD + kDecMaxD * (kDecMaxD + 1) / 2;
+constexpr int kDecRows = 32;    // state rows per reduction tile
+
+__device__ __forceinline__ float load_elem(const void* base, size_t i, bool f32) {
+  return f32 ? static_cast<const float*>(base)[i] : bf16_bits_to_f32(static_cast<const uint16_t*>(base)[i]);
+}
+
+// Feature f of phi(x) (reference order), x in LDS.
+__device__ __forceinline__ float feature(const float* x, int f, int d, float r4, float rsq, float rd) {
+  if (f == 0) return 1.f;
+  if (f <= d) return x[f - 1] * r4;
+  if (f <= 2 * d) {
+    const float t = x[f - 1 - d];
+    return t * t * rsq;
+  }
+  int t = f - 1 - 2 * d, i = 0;
+  while (t >= d - 1 - i) {   // row i of the strict upper triangle holds d - 1 - i pairs
+    t -= d - 1 - i;
+    ++i;
+  }
+  return x[i] * x[i + 1 + t] * rd;
+}
+
+__global__ __launch_bounds__(kDecThreads) void based_decode_kernel(const DecodeParams p) {
+  __shared__ float xq[kDecMaxD], xk[kDecMaxD], vv[kDecMaxC];
+  __shared__ float phq[kDecMaxF], phk[kDecMaxF];
+  __shared__ float tile[kDecRows * kDecMaxC];
+  const int bh = blockIdx.x, tid = threadIdx.x;
+  const int d = p.d, dv = p.dv, F = p.F, C = dv + 1;
+  if (tid < d) {
+    xq[tid] = load_elem(p.q, (size_t)bh * d + tid, p.in_f32);
+    xk[tid] = load_elem(p.k, (size_t)bh * d + tid, p.in_f32);
+  }
+  if (tid < dv) vv[tid] = load_elem(p.v, (size_t)bh * dv + tid, p.in_f32);
+  if (tid == 0) vv[dv] = 1.f;
+  __syncthreads();
+  const float rd = 1.0f / sqrtf((float)d), r4 = sqrtf(rd), rsq = rd * 0.70710678118654752f;
+  for (int f = tid; f < F; f += kDecThreads) {
+    phq[f] = feature(xq, f, d, r4, rsq, rd);
+    phk[f] = feature(xk, f, d, r4, rsq, rd);
+  }
+  __syncthreads();
+
+  // The state sweeps linearly (coalesced) in tiles of kDecRows rows: every element is updated
+  // in place and its phi(q)-weighted value parked in LDS, then thread c < C adds the tile's
+  // column c in row order.
+  float* __restrict__ st = p.state + (size_t)bh * F * C;
+  float colsum = 0.f;
+  for (int r0 = 0; r0 < F; r0 += kDecRows) {
+    const int ne = min(kDecRows, F - r0) * C;
+    float* __restrict__ base = st + (size_t)r0 * C;
+    for (int e = tid; e < ne; e += kDecThreads) {
+      const int fr = e / C, c = e - fr * C;
+      const float s = __builtin_fmaf(phk[r0 + fr], vv[c], base[e]);
+      base[e] = s;
+      tile[e] = phq[r0 + fr] * s;
+    }
+    __syncthreads();
+    if (tid < C)
+      for (int e = tid; e < ne; e += C) colsum += tile[e];
+    __syncthreads();
+  }
+  __shared__ float den;
+  if (tid == dv) den = colsum;
+  __syncthreads();
+  if (tid < dv) {
+    const float y = p.normalize ? colsum / (den + p.eps) : colsum;
+    const size_t o = (size_t)bh * dv + tid;
+    if (p.out_f32)
+      static_cast<float*>(p.out)[o] = y;
+    else
+      static_cast<uint16_t*>(p.out)[o] = f32_to_bf16_bits(y);
+  }
+}
+
+}  // namespace
+
+bool decode_shape(int d, int dv) { return d >= 1 && d <= kDecMaxD && dv >= 1 && dv + 1 <= kDecMaxC; }
+
+int launch_decode_step(const DecodeArgs& a, hipStream_t stream) {
+  DecodeParams p{};
+  p.q = a.q;
+  p.k = a.k;
+  p.v = a.v;
+  p.state = a.state;
+  p.out = a.out;
+  p.BH = a.BH;
+  p.d = a.d;
+  p.dv = a.dv;
+  p.F = 1 + a.d + a.d * (a.d + 1) / 2;
+  p.eps = a.eps;
+  p.normalize = a.normalize ? 1 : 0;
+  p.in_f32 = a.in_f32 ? 1 : 0;
+  p.out_f32 = a.out_f32 ? 1 : 0;
+  hipLaunchKernelGGL(based_decode_kernel, dim3((unsigned)a.BH), dim3(kDecThreads), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
+}  // namespace la

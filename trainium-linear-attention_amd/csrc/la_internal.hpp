@@ -59,6 +59,17 @@ struct IdentityArgs {
   bool out_f32;
 };
 
+struct DecodeArgs {
+  const void* q;       // (BH, d)
+  const void* k;       // (BH, d)
+  const void* v;       // (BH, dv)
+  float* state;        // (BH, F, dv + 1) fp32, updated in place
+  void* out;           // (BH, dv)
+  int BH, d, dv;
+  float eps;
+  bool normalize, in_f32, out_f32;
+};
+
 struct FeatureMapArgs {
   const void* x;
   void* out;
@@ -78,6 +89,8 @@ int launch_feature_map(const FeatureMapArgs& a, hipStream_t stream);
 bool identity_shape(int d, int dv);
 size_t identity_workspace_bytes(int BH, int N, int d, int dv);
 int launch_identity(const IdentityArgs& a, hipStream_t stream);
+bool decode_shape(int d, int dv);
+int launch_decode_step(const DecodeArgs& a, hipStream_t stream);
 
 // Work-group order for causal query blocks: heaviest (last) blocks first over all the heads an
 // XCD owns, so that greedy dispatch as slots free up balances the causal triangle (a head-major

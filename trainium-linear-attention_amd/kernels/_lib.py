@@ -47,6 +47,8 @@ _SIGNATURES = {
                                        _c_int, _c_int, _c_int, _c_int, _c_float, _c_void]),
     "la_sliding_window_fwd_add": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int,
                                            _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_void]),
+    "la_based_decode_step": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int, _c_int,
+                                      _c_int, _c_int, _c_float, _c_int, _c_void]),
     "la_identity_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "la_identity_linear_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int, _c_int,
                                         _c_int, _c_int, _c_float, _c_void, _c_size, _c_void]),

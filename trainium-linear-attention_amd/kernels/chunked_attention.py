@@ -30,6 +30,7 @@ from . import _lib
 from .pytorch_attention import _as_kernel_input, _check_qkv, _compute_dtype
 
 __all__ = ["taylor_feature_map", "feature_dim", "chunked_nki_numerator", "chunked_based_attn", "based_chunked",
+           "based_decode_step",
            "chunked_supported"]
 
 
@@ -95,6 +96,44 @@ def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, 
     if out.dtype != odt:
         out = out.to(odt)
     return (out, state) if return_state else out
+
+
+def based_decode_step(q, k, v, state, eps=1e-6, normalize=True):
+    """One decode step on an exported state (``based_chunked(..., return_state=True)``) through
+    ``la_based_decode_step``: ``state`` (b, h, F, dv + 1) fp32 = [S | z] is updated in place with
+    the new token, ``[S | z] += phi(k) [v | 1]``, and the token's output is returned,
+    ``phi(q) S / (phi(q) z + eps)`` (the numerator with ``normalize=False``), in q.dtype.
+
+    q, k: (b, h, d) or (b, h, 1, d); v: (b, h, dv) or (b, h, 1, dv) -- one token per head.
+    The reference has no decode path; this continues the chunk recurrence of
+    kernels/nki_attention_chunked.py:65-109 one token at a time.
+    """
+    squeeze = q.dim() == 4
+    if squeeze:
+        if q.shape[2] != 1 or k.shape[2] != 1 or v.shape[2] != 1:
+            raise _lib.BasedLAError("decode takes one token per head: shape (b, h, 1, d)")
+        q, k, v = q[:, :, 0], k[:, :, 0], v[:, :, 0]
+    _lib.require_gpu(q, k, v, state)
+    if q.dim() != 3 or k.shape != q.shape or v.shape[:2] != q.shape[:2]:
+        raise _lib.BasedLAError("q, k must be (b, h, d) and v (b, h, dv)")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise _lib.BasedLAError("q, k, v must share one dtype")
+    b, h, d = q.shape
+    dv = v.shape[-1]
+    if state.dtype != torch.float32 or tuple(state.shape) != (b, h, feature_dim(d), dv + 1) \
+            or not state.is_contiguous():
+        raise _lib.BasedLAError(f"state must be contiguous fp32 {(b, h, feature_dim(d), dv + 1)}")
+    cdt = _compute_dtype(q.dtype)
+    kdt = q.dtype if q.dtype in (torch.float32, torch.bfloat16) else torch.float32
+    qc, kc, vc = (_as_kernel_input(x, cdt) for x in (q, k, v))
+    out = torch.empty(b, h, dv, dtype=kdt, device=q.device)
+    rc = _lib.lib().la_based_decode_step(
+        _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.dtype_code(cdt), _lib.ptr(state), _lib.ptr(out),
+        _lib.dtype_code(kdt), b, h, d, dv, float(eps), 1 if normalize else 0, _lib.stream_of(q))
+    _lib.check(rc, "la_based_decode_step")
+    if out.dtype != q.dtype:
+        out = out.to(q.dtype)
+    return out.unsqueeze(2) if squeeze else out
 
 
 def chunked_nki_numerator(q, k, v, chunk_size=64):
