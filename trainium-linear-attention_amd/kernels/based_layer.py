@@ -16,9 +16,9 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, pytorch_attention
 from .chunked_attention import based_chunked, chunked_supported
-from .pytorch_attention import CHUNKED_MIN_T, _check_qkv, _compute_dtype, based_parallel
+from .pytorch_attention import _check_qkv, _compute_dtype, based_parallel
 from .sliding_attention import _sliding
 
 __all__ = ["based_layer_attn"]
@@ -39,7 +39,7 @@ def based_layer_attn(q, k, v, window_size=64, q_sw=None, k_sw=None, eps=1e-6):
     if int(window_size) < 1:
         raise _lib.BasedLAError("window_size must be >= 1")
     t, d, dv = q.shape[-2], q.shape[-1], v.shape[-1]
-    if t >= CHUNKED_MIN_T and chunked_supported(d, dv, _compute_dtype(q.dtype)):
+    if t >= pytorch_attention.CHUNKED_MIN_T and chunked_supported(d, dv, _compute_dtype(q.dtype)):
         lin = based_chunked(q, k, v, eps=eps, normalize=True, out_dtype=torch.float32)
     else:
         lin = based_parallel(q, k, v, eps=eps, out_dtype=torch.float32)
