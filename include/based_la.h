@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 4
+#define LA_ABI_VERSION 5
 
 /* element types */
 #define LA_F32 0
@@ -38,6 +38,7 @@ extern "C" {
 #define LA_ERR_WORKSPACE (-6)
 #define LA_ERR_NO_DEVICE (-7)
 #define LA_ERR_BAD_ALIGNMENT (-8)
+#define LA_ERR_OVERLAP (-9)
 
 /* Version of this ABI (LA_ABI_VERSION). */
 int la_abi_version(void);
@@ -108,6 +109,21 @@ int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dty
                          float scale, float eps, int normalize,
                          void* workspace, size_t workspace_bytes, float* state_out_or_null,
                          void* hip_stream);
+
+/*
+ * la_based_chunked_fwd continuing from an initial state: the sequence is the prev_tokens
+ * tokens summarised by state_in followed by these N.  state_in: fp32 (B,H,F,dv+1) in the layout
+ * of state_out (as exported by an earlier call, or updated by la_based_decode_step), not
+ * overlapping state_out (LA_ERR_OVERLAP); prev_tokens: its token count (z[0], the same for every
+ * head).  Output rows are tokens prev_tokens .. prev_tokens + N - 1 of the whole sequence;
+ * state_out (optional) covers all prev_tokens + N.  No reference counterpart (the reference
+ * starts every call from a zero state, kernels/nki_attention_chunked.py:66-69).
+ */
+int la_based_chunked_fwd_continue(const void* q, const void* k, const void* v, int in_dtype,
+                                  void* out, int out_dtype, int B, int H, int N, int d, int dv,
+                                  int chunk, float scale, float eps, int normalize,
+                                  void* workspace, size_t workspace_bytes, const float* state_in,
+                                  long long prev_tokens, float* state_out_or_null, void* hip_stream);
 
 /*
  * Causal sliding-window softmax attention.

@@ -26,7 +26,7 @@ def _lib():
 def test_header_declares_expected_entry_points():
     assert _declared() == sorted([
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
-        "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_fwd", "la_sliding_window_fwd",
+        "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_fwd", "la_based_chunked_fwd_continue", "la_sliding_window_fwd",
         "la_sliding_window_fwd_add", "la_based_decode_step", "la_identity_workspace_bytes", "la_identity_linear_fwd",
         "la_taylor_feature_map"])
 
@@ -39,8 +39,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib()
-    assert lib.la_abi_version() == 4
-    for code in range(-8, 1):
+    assert lib.la_abi_version() == 5
+    for code in range(-9, 1):
         s = lib.la_status_string(code).decode()
         assert s and s != "unknown status"
 
@@ -99,6 +99,25 @@ def test_sliding_add_argument_errors():
     assert call(12, 0) == -4                       # window
     assert call(10, 129) == -5                     # d
     assert call(9, 0) == 0                         # N = 0: nothing to launch
+
+
+def test_chunked_continue_argument_errors():
+    lib = _lib()
+    f = lib.la_based_chunked_fwd_continue
+    need = lib.la_based_chunked_workspace_bytes(1, 1, 8, 16, 64, 64)
+    S = ctypes.c_void_p(1 << 20)
+    ok = [P, P, P, 1, P, 1, 1, 1, 8, 16, 64, 64, 0.25, 1e-6, 1, P, need, S, 100, None, None]
+
+    def call(i, x):
+        a = list(ok)
+        a[i] = x
+        return f(*a)
+
+    assert call(17, None) == -1                                   # state_in required
+    assert call(17, ctypes.c_void_p((1 << 20) + 2)) == -8         # not 4-byte aligned
+    assert call(18, -1) == -4                                     # prev_tokens
+    assert call(19, ctypes.c_void_p((1 << 20) + 4096)) == -9      # state_out overlaps state_in
+    assert call(8, 0) == 0                                        # N = 0
 
 
 def test_decode_argument_errors():

@@ -142,6 +142,9 @@ struct ChunkParams {
   float alpha, beta;                 // q~ = alpha q, k~ = beta k
   float eps;
   float st_fac[4];                   // internal -> reference feature factors (state export)
+  float st_inv[4];                   // their inverses (initial state import)
+  const float* state_in;             // optional initial state, reference basis (BH, 153, dv + 1)
+  float prev_tokens;                 // tokens summarised by state_in (0 without one)
   int normalize, out_f32, vec_out;
 };
 
@@ -483,16 +486,67 @@ __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_k
 }
 
 // -------------------------------------------------------------------------------------------
+// Initial state (continuation): the caller's [S | z] in the reference feature basis
+// (benchmarks/chunked_attention_benchmark.py:34-53 order), converted to the internal basis in
+// slot P - 1 of every head: S^T slot f = S_ref[ref(f)] / factor (fp16 [64][NF]); the Gram matrix
+// of [k~ | 1] in the accumulator layout [64 lanes][16], entry (i, j) = the k-sum of the feature
+// it carries / factor: (16, 16) the count, (i, 16) linear, (i, i) square, (i, j) pair -- the
+// inverse of the state export at the end of output_wave.
+__global__ __launch_bounds__(256) void chunked_import_kernel(const ChunkParams p) {
+  const int bh = blockIdx.x, tid = threadIdx.x, dv = p.dv;
+  const float* si = p.state_in + (size_t)bh * 153 * (dv + 1);
+  const size_t slot = (size_t)bh * p.P + (p.P - 1);
+  uint16_t* ws = p.wsS + slot * (64 * NF);
+  for (int idx = tid; idx < 64 * NF; idx += 256) {
+    const int c = idx / NF, f = idx - c * NF;
+    float x = 0.f;
+    if (c < dv && f < 160) {
+      const RefFeat rf = ref_feature(f);
+      if (rf.ref >= 0) x = si[(size_t)rf.ref * (dv + 1) + c] * p.st_inv[rf.fac];
+    }
+    ws[idx] = (uint16_t)(pack_f16x2(x, 0.f) & 0xffffu);
+  }
+  float* g = p.wsG + slot * 1024;
+  for (int idx = tid; idx < 1024; idx += 256) {
+    const int lane = idx >> 4, e = idx & 15, r = lane & 31, h = lane >> 5;
+    const int row = 8 * (e >> 2) + 4 * h + (e & 3), col = r;
+    float x = 0.f;
+    if (row <= 16 && col <= 16) {
+      const int lo = row < col ? row : col, hi = row < col ? col : row;
+      if (lo == 16) {
+        x = si[dv];                                                               // count
+      } else if (hi == 16) {
+        x = si[(size_t)(1 + lo) * (dv + 1) + dv] * p.st_inv[1];                  // linear
+      } else if (lo == hi) {
+        x = si[(size_t)(17 + lo) * (dv + 1) + dv] * p.st_inv[2];                 // square
+      } else {
+        x = si[(size_t)(33 + lo * (31 - lo) / 2 + (hi - lo - 1)) * (dv + 1) + dv] * p.st_inv[3];   // pair
+      }
+    }
+    g[idx] = x;
+  }
+}
+
+// -------------------------------------------------------------------------------------------
 // Kernel 2: exclusive prefixes over segments, in place: afterwards slot p - 1 holds the sum of
 // the increments of segments 0 .. p-1.  Thread (head, 8-byte unit), fp32 accumulation, the loads
 // of up to 16 segments in flight at once.
+// With an initial state the scan starts from slot P - 1 (written by chunked_import_kernel).
 __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p) {
   constexpr int US = 64 * NF / 4, UG = 1024 / 2;   // 8-byte units of S^T (fp16) and G (fp32)
   const int e = blockIdx.x * 256 + threadIdx.x, bh = blockIdx.y;
   const int nseg = p.P - 1;
+  const bool init = p.state_in != nullptr;
   if (e < US) {
     uint16_t* base = p.wsS + (size_t)bh * p.P * (64 * NF) + 4 * (size_t)e;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    if (init) {
+      const u32x2 x0 = *reinterpret_cast<const u32x2*>(base + (size_t)nseg * (64 * NF));
+      acc[0] = f16_lo_to_f32(x0[0]);
+      acc[1] = f16_hi_to_f32(x0[0]);
+      acc[2] = f16_lo_to_f32(x0[1]);
+      acc[3] = f16_hi_to_f32(x0[1]);
+    }
     for (int s0 = 0; s0 < nseg; s0 += 16) {
       u32x2 x[16];
 #pragma unroll
@@ -511,7 +565,7 @@ __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p
     }
   } else if (e < US + UG) {
     float* base = p.wsG + (size_t)bh * p.P * 1024 + 2 * (size_t)(e - US);
-    f32x2 acc = {0.f, 0.f};
+    f32x2 acc = init ? *reinterpret_cast<const f32x2*>(base + (size_t)nseg * 1024) : (f32x2){0.f, 0.f};
     for (int s0 = 0; s0 < nseg; s0 += 16) {
       f32x2 x[16];
 #pragma unroll
@@ -614,8 +668,10 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
   StageRegs st;
   StageConv cv;
   stage_load<VEC, true>(st, p, qh, kh, vh, c0 * CH, lane, W);
-  if (seg > 0) {
-    const size_t slot = (size_t)bh * p.P + (seg - 1);
+  if (seg > 0 || p.state_in != nullptr) {
+    // prefix of the earlier segments (with the caller's initial state, when there is one); the
+    // first segment's is slot P - 1, which holds the initial state alone
+    const size_t slot = (size_t)bh * p.P + (seg > 0 ? seg - 1 : p.P - 1);
     const uint16_t* ws = p.wsS + slot * (64 * NF);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -753,7 +809,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
     {
       float x = dden + rs;
       x += __shfl_xor(x, 32);
-      const float den = (float)row0 + 0.5f * x;
+      const float den = (float)row0 + p.prev_tokens + 0.5f * x;
       // v_rcp_f32 (1 ulp) instead of an IEEE division, and a select, keep this branch-free
       const float sc = p.normalize ? 0.5f * __builtin_amdgcn_rcpf(den + p.eps) : 0.5f;
       const int row = row0 + 32 * W + r;
@@ -848,7 +904,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
         kt_row_dim(kr.a, da, fa);
         kt_row_dim(kr.b, db, fb);
         const float z = fa * fb * G32[da * 33 + db];
-        so[(size_t)rf.ref * (dv + 1) + dv] = rf.ref == 0 ? (float)N : z * p.st_fac[rf.fac];
+        so[(size_t)rf.ref * (dv + 1) + dv] = rf.ref == 0 ? (float)N + p.prev_tokens : z * p.st_fac[rf.fac];
       }
     }
   }
@@ -913,7 +969,8 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
   // q~ = alpha q, k~ = beta k with alpha beta = scale; sigma moves magnitude from the state
   // (sums over up to N tokens) to the q side so that it stays well inside the fp16 range.
   int sigma = 0;
-  while ((1 << (sigma + 10)) < a.N && sigma < 12) sigma += 2;
+  const double total = (double)a.N + (double)a.prev_tokens;   // tokens the state will sum over
+  while ((double)(1 << (sigma + 10)) < total && sigma < 12) sigma += 2;
   const double rc = sqrt((double)a.scale);
   p.alpha = (float)(rc * ldexp(1.0, sigma / 2));
   p.beta = (float)(rc * ldexp(1.0, -sigma / 2));
@@ -922,11 +979,19 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
   p.st_fac[1] = (float)ldexp(1.0, sigma / 2);
   p.st_fac[2] = (float)(ldexp(1.0, sigma) / sqrt(2.0));
   p.st_fac[3] = (float)ldexp(1.0, sigma);
+  for (int i = 0; i < 4; ++i) p.st_inv[i] = (float)(1.0 / (double)p.st_fac[i]);
+  p.state_in = a.state_in;
+  p.prev_tokens = (float)a.prev_tokens;
   p.eps = a.eps;
   p.normalize = a.normalize ? 1 : 0;
   p.out_f32 = a.out_f32 ? 1 : 0;
   const bool vec_v = (a.dv % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 15) == 0);
   p.vec_out = (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0);
+  if (a.state_in != nullptr) {
+    hipLaunchKernelGGL(chunked_import_kernel, dim3((unsigned)a.BH), dim3(256), 0, stream, p);
+    const int e = (int)hipGetLastError();
+    if (e != 0) return e;
+  }
   if (P > 1) {
     const dim3 grid((unsigned)((a.BH * (P - 1) + SEG_PER_WG - 1) / SEG_PER_WG));
     const dim3 block(64 * NWAVE_SEG * SEG_PER_WG);

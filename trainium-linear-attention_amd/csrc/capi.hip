@@ -47,6 +47,7 @@ const char* la_status_string(int status) {
     case LA_ERR_WORKSPACE: return "workspace too small";
     case LA_ERR_NO_DEVICE: return "no HIP device";
     case LA_ERR_BAD_ALIGNMENT: return "tensor pointer not aligned to its element size";
+    case LA_ERR_OVERLAP: return "input and output buffers overlap";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
@@ -130,9 +131,10 @@ size_t la_based_chunked_workspace_bytes(int B, int H, int N, int d, int dv, int 
   return la::chunked_workspace_bytes(B * H, N, d, dv, chunk);
 }
 
-int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
-                         int H, int N, int d, int dv, int chunk, float scale, float eps, int normalize,
-                         void* workspace, size_t workspace_bytes, float* state_out_or_null, void* hip_stream) {
+static int chunked_common(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
+                          int H, int N, int d, int dv, int chunk, float scale, float eps, int normalize,
+                          void* workspace, size_t workspace_bytes, const float* state_in, long long prev_tokens,
+                          float* state_out_or_null, void* hip_stream) {
   int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
   if (rc != LA_OK) return rc;
   if (!finite_f(scale) || !(scale > 0.f) || !finite_f(eps) || eps < 0.f) return LA_ERR_BAD_SCALAR;
@@ -142,12 +144,23 @@ int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dty
   if (need == (size_t)-1) return LA_ERR_UNSUPPORTED_DIM;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
   if (state_out_or_null != nullptr && (reinterpret_cast<uintptr_t>(state_out_or_null) & 3)) return LA_ERR_BAD_ALIGNMENT;
+  if (state_in != nullptr) {
+    if (reinterpret_cast<uintptr_t>(state_in) & 3) return LA_ERR_BAD_ALIGNMENT;
+    if (prev_tokens < 0) return LA_ERR_BAD_SCALAR;
+    // the last segment writes state_out while other segments may still read state_in
+    const char* i0 = reinterpret_cast<const char*>(state_in);
+    const char* o0 = reinterpret_cast<const char*>(state_out_or_null);
+    const size_t bytes = (size_t)B * H * 153 * (size_t)(dv + 1) * 4;
+    if (o0 != nullptr && i0 < o0 + bytes && o0 < i0 + bytes) return LA_ERR_OVERLAP;
+  }
   la::ChunkedArgs a{};
   a.q = q;
   a.k = k;
   a.v = v;
   a.out = out;
   a.state_out = state_out_or_null;
+  a.state_in = state_in;
+  a.prev_tokens = state_in != nullptr ? prev_tokens : 0;
   a.workspace = workspace;
   a.workspace_bytes = workspace_bytes;
   a.BH = B * H;
@@ -161,6 +174,23 @@ int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dty
   a.in_f32 = in_dtype == LA_F32;
   a.out_f32 = out_dtype == LA_F32;
   return la::launch_based_chunked(a, static_cast<hipStream_t>(hip_stream));
+}
+
+int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
+                         int H, int N, int d, int dv, int chunk, float scale, float eps, int normalize,
+                         void* workspace, size_t workspace_bytes, float* state_out_or_null, void* hip_stream) {
+  return chunked_common(q, k, v, in_dtype, out, out_dtype, B, H, N, d, dv, chunk, scale, eps, normalize, workspace,
+                        workspace_bytes, nullptr, 0, state_out_or_null, hip_stream);
+}
+
+int la_based_chunked_fwd_continue(const void* q, const void* k, const void* v, int in_dtype, void* out,
+                                  int out_dtype, int B, int H, int N, int d, int dv, int chunk, float scale,
+                                  float eps, int normalize, void* workspace, size_t workspace_bytes,
+                                  const float* state_in, long long prev_tokens, float* state_out_or_null,
+                                  void* hip_stream) {
+  if (state_in == nullptr && (long long)B * H * N != 0) return LA_ERR_NULL_POINTER;
+  return chunked_common(q, k, v, in_dtype, out, out_dtype, B, H, N, d, dv, chunk, scale, eps, normalize, workspace,
+                        workspace_bytes, state_in, prev_tokens, state_out_or_null, hip_stream);
 }
 
 size_t la_identity_workspace_bytes(int B, int H, int N, int d, int dv) {

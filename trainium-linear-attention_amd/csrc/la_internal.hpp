@@ -40,6 +40,8 @@ struct ChunkedArgs {
   const void* v;
   void* out;
   float* state_out;    // optional, (BH, F, dv + 1) fp32
+  const float* state_in;   // optional initial state, same layout
+  long long prev_tokens;   // tokens summarised by state_in
   void* workspace;
   size_t workspace_bytes;
   int BH, N, d, dv, chunk;

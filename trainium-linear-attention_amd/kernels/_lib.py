@@ -47,6 +47,9 @@ _SIGNATURES = {
                                        _c_int, _c_int, _c_int, _c_int, _c_float, _c_void]),
     "la_sliding_window_fwd_add": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int,
                                            _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_void]),
+    "la_based_chunked_fwd_continue": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
+                                               _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int, _c_void,
+                                               _c_size, _c_void, ctypes.c_longlong, _c_void, _c_void]),
     "la_based_decode_step": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int, _c_int,
                                       _c_int, _c_int, _c_float, _c_int, _c_void]),
     "la_identity_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
@@ -55,7 +58,7 @@ _SIGNATURES = {
     "la_taylor_feature_map": (_c_int, [_c_void, _c_int, _c_void, _c_int, ctypes.c_longlong, _c_int, _c_void]),
 }
 
-EXPECTED_ABI = 4
+EXPECTED_ABI = 5
 
 
 class BasedLAError(RuntimeError):

@@ -59,11 +59,14 @@ def chunked_supported(d: int, dv: int, dtype: torch.dtype) -> bool:
 
 
 def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, out_dtype=None,
-                  return_state=False):
+                  return_state=False, state_in=None, prev_tokens=None):
     """Chunked recurrent BASED attention through ``la_based_chunked_fwd``.
 
     ``return_state`` also returns the final per-head state in the reference feature basis:
     (b, h, F, dv + 1) fp32 = [sum_u phi(k_u) v_u^T | sum_u phi(k_u)].
+    ``state_in`` (same layout, e.g. an earlier call's state) continues a sequence: these tokens
+    follow the ``prev_tokens`` tokens it summarises (default: its count entry z[0] of head 0,
+    read back to the host), through ``la_based_chunked_fwd_continue``; it is not modified.
     """
     _check_qkv(q, k, v)
     if int(chunk_size) < 1:
@@ -72,8 +75,8 @@ def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, 
     dv = v.shape[-1]
     cdt = _compute_dtype(q.dtype)
     if not chunked_supported(d, dv, cdt):
-        if return_state:
-            raise _lib.BasedLAError("state export needs the chunked kernel (bf16, d = 16, dv <= 64)")
+        if return_state or state_in is not None:
+            raise _lib.BasedLAError("state export and import need the chunked kernel (bf16, d = 16, dv <= 64)")
         from .pytorch_attention import based_parallel
         return based_parallel(q, k, v, eps=eps, scale=scale, normalize=normalize, out_dtype=out_dtype)
     odt = q.dtype if out_dtype is None else out_dtype
@@ -88,11 +91,24 @@ def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, 
         raise _lib.BasedLAError(f"chunked kernel does not support d={d}, dv={dv}, chunk={chunk_size}")
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     state = torch.empty(b, h, feature_dim(d), dv + 1, dtype=torch.float32, device=q.device) if return_state else None
-    rc = L.la_based_chunked_fwd(
-        _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.dtype_code(cdt), _lib.ptr(out), _lib.dtype_code(kdt),
-        b, h, t, d, dv, int(chunk_size), float(scale), float(eps), 1 if normalize else 0,
-        _lib.ptr(ws), ws_bytes, _lib.ptr(state), _lib.stream_of(q))
-    _lib.check(rc, "la_based_chunked_fwd")
+    if state_in is None:
+        rc = L.la_based_chunked_fwd(
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.dtype_code(cdt), _lib.ptr(out), _lib.dtype_code(kdt),
+            b, h, t, d, dv, int(chunk_size), float(scale), float(eps), 1 if normalize else 0,
+            _lib.ptr(ws), ws_bytes, _lib.ptr(state), _lib.stream_of(q))
+        _lib.check(rc, "la_based_chunked_fwd")
+    else:
+        _lib.require_gpu(q, state_in)
+        if state_in.dtype != torch.float32 or tuple(state_in.shape) != (b, h, feature_dim(d), dv + 1):
+            raise _lib.BasedLAError(f"state_in must be fp32 {(b, h, feature_dim(d), dv + 1)}")
+        si = state_in.contiguous()
+        if prev_tokens is None:
+            prev_tokens = int(round(float(si[0, 0, 0, dv].item()))) if b * h > 0 else 0
+        rc = L.la_based_chunked_fwd_continue(
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.dtype_code(cdt), _lib.ptr(out), _lib.dtype_code(kdt),
+            b, h, t, d, dv, int(chunk_size), float(scale), float(eps), 1 if normalize else 0,
+            _lib.ptr(ws), ws_bytes, _lib.ptr(si), int(prev_tokens), _lib.ptr(state), _lib.stream_of(q))
+        _lib.check(rc, "la_based_chunked_fwd_continue")
     if out.dtype != odt:
         out = out.to(odt)
     return (out, state) if return_state else out
