@@ -1,5 +1,7 @@
 """GPU parity of the sliding-window softmax kernel (la_sliding_window_fwd) against the oracle."""
 
+import math
+
 import pytest
 import torch
 
@@ -79,10 +81,11 @@ def test_config4_bf16():
 
 
 @pytest.mark.parametrize("d,dv", [(16, 32), (16, 64), (32, 32), (32, 64), (64, 32), (64, 64)])
-@pytest.mark.parametrize("W", [1, 37, 64, 65])
+@pytest.mark.parametrize("W", [1, 37, 64, 65, 66, 100, 128, 129])
 def test_resident_window_shapes(d, dv, W):
-    """W <= 65 with d in {16, 32, 64} and dv in {32, 64} runs the LDS-resident kernel; ragged N
-    so that the last 256-query tile and its key blocks are partial."""
+    """W <= 129 with d in {16, 32, 64} and dv in {32, 64} runs the LDS-resident kernel (one extra
+    key block per tile above W = 65); ragged N so that the last 256-query tile and its key blocks
+    are partial."""
     K = _kernels()
     q, k, v = rand_qkv(1, 3, 333, d, dv, seed=d * 7 + dv + W, dtype=torch.bfloat16)
     y = K.sliding_window_attn(*to_dev(q, k, v), window_size=W, out_dtype=torch.float32)
@@ -90,17 +93,24 @@ def test_resident_window_shapes(d, dv, W):
     assert err(y, want) < TOL_BF16
 
 
-def test_resident_matches_streaming_path():
-    """The same inputs through the resident kernel (16-byte aligned) and through the streaming
-    kernel (q moved off 16-byte alignment, which the resident kernel requires)."""
-    K = _kernels()
-    q, k, v = to_dev(*rand_qkv(2, 2, 700, 64, 64, seed=9, dtype=torch.bfloat16))
-    y_res = K.sliding_window_attn(q, k, v, window_size=64, out_dtype=torch.float32)
-    buf = torch.empty(q.numel() + 4, dtype=q.dtype, device=q.device)
-    q_off = buf[4:].view(q.shape)
-    q_off.copy_(q)
-    assert q_off.data_ptr() % 16 != 0
-    y_str = K.sliding_window_attn(q_off, k, v, window_size=64, out_dtype=torch.float32)
-    want = ref.sliding_dense(q.cpu(), k.cpu(), v.cpu(), window_size=64)
-    assert err(y_res, want) < TOL_BF16 and err(y_str, want) < TOL_BF16
-    assert (y_res - y_str).abs().max().item() < 1e-3
+@pytest.mark.parametrize("W", [64, 65, 66, 128, 129])
+def test_resident_matches_streaming_path(W):
+    """The same inputs through the resident kernel (16-byte aligned output) and through the
+    streaming kernel (fp32 output 4 bytes off 16-byte alignment, which the resident kernel
+    requires), both through the C ABI."""
+    from kernels import _lib
+    L = _lib.lib()
+    B, H, N, d, dv = 2, 2, 700, 64, 64
+    q, k, v = to_dev(*rand_qkv(B, H, N, d, dv, seed=9 + W, dtype=torch.bfloat16))
+    st = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for off in (0, 1):
+        buf = torch.empty(B * H * N * dv + 4, dtype=torch.float32, device="cuda")
+        out = buf[off:off + B * H * N * dv].view(B, H, N, dv)
+        assert (out.data_ptr() % 16 == 0) == (off == 0)
+        assert L.la_sliding_window_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), 1, out.data_ptr(), 0, B, H, N, d, dv,
+                                       W, 1.0 / math.sqrt(d), st) == 0
+        outs.append(out.clone())
+    want = ref.sliding_dense(q.cpu(), k.cpu(), v.cpu(), window_size=W)
+    assert err(outs[0], want) < TOL_BF16 and err(outs[1], want) < TOL_BF16
+    assert (outs[0] - outs[1]).abs().max().item() < 1e-3

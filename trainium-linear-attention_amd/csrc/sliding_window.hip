@@ -200,8 +200,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 8 ? 1
   }
 }
 
-// W <= 65, d % 16 == 0, dv % 32 == 0, q, k, v 16-byte aligned: a 128-query tile needs at most
-// three 64-key blocks, so all of them are copied global -> LDS at once with buffer_load ... lds
+// W <= 64 XB + 1, d % 16 == 0, dv % 32 == 0, q, k, v 16-byte aligned: a tile of 32 NW queries
+// needs at most NW / 2 + XB 64-key blocks, so all of them are copied global -> LDS at once with buffer_load ... lds
 // (K and V row-major, the 16-byte chunks of each row XOR-swizzled by the row index against bank
 // conflicts) and the waves then run without further synchronisation.  K fragments (A operand of
 // S^T = K Q^T) are ds_read_b128; V^T fragments (A operand of O^T = V^T P^T) come straight from
@@ -214,11 +214,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 8 ? 1
 __device__ __forceinline__ int swz_k(int row, int nch) { return row % nch; }
 __device__ __forceinline__ int swz_v(int row, int nch) { return (row >> 1) % nch; }
 
-template <int KS, int MT, int NW>
+template <int KS, int MT, int NW, int XB>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 4 : 3))) void sliding_resident_kernel(
     const SlidingParams p) {
   constexpr int DK = 16 * KS, DV = 32 * MT, BM = 32 * NW;
-  constexpr int kResBlocks = BM / BN + 1;   // key blocks a tile needs for W <= 65
+  constexpr int kResBlocks = BM / BN + XB;   // key blocks a tile needs for W <= 64 XB + 1
   constexpr int KCH = DK / 8, VCH = DV / 8;                 // 16-byte chunks per K / V row
   constexpr int KU = BN * DK * 2 / 1024, VU = BN * DV * 2 / 1024;   // 1 KB copy units per block
   constexpr int NU = kResBlocks * (KU + VU), UPW = (NU + NW - 1) / NW;
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 8
   const int q0 = qb * BM;
   const int jlo = max(0, q0 - W + 1) / BN;
   const int jhi = min((N - 1) / BN, (q0 + BM - 1) / BN);
-  const int nbk = jhi - jlo + 1;   // <= kResBlocks for W <= 65
+  const int nbk = jhi - jlo + 1;   // <= kResBlocks for W <= 64 XB + 1
   const size_t hrow = (size_t)bh * N;
   const uint16_t* __restrict__ qg = p.q + hrow * DK;
   const uint16_t* __restrict__ kg = p.k + hrow * DK;
@@ -397,10 +397,15 @@ int launch_sl(SlidingParams p, bool vec, hipStream_t stream) {
 
 template <int KS, int MT>
 int launch_resident(SlidingParams p, hipStream_t stream) {
-  constexpr int NW = 8;
-  p.nqb = (p.N + 32 * NW - 1) / (32 * NW);
-  hipLaunchKernelGGL((sliding_resident_kernel<KS, MT, NW>), dim3((unsigned)(p.nqb * p.BH)), dim3(64 * NW), 0, stream,
-                     p);
+  if (p.window <= BN + 1) {
+    constexpr int NW = 8;
+    p.nqb = (p.N + 32 * NW - 1) / (32 * NW);
+    hipLaunchKernelGGL((sliding_resident_kernel<KS, MT, NW, 1>), dim3((unsigned)(p.nqb * p.BH)), dim3(64 * NW), 0, stream, p);
+  } else {
+    constexpr int NW = 4;
+    p.nqb = (p.N + 32 * NW - 1) / (32 * NW);
+    hipLaunchKernelGGL((sliding_resident_kernel<KS, MT, NW, 2>), dim3((unsigned)(p.nqb * p.BH)), dim3(64 * NW), 0, stream, p);
+  }
   return (int)hipGetLastError();
 }
 
@@ -445,7 +450,7 @@ int launch_sliding_window(const SlidingArgs& a, hipStream_t stream) {
   const bool vec = (a.d % 8 == 0) && (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.k) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 7) == 0) &&
                    ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0);
-  const bool resident = a.window <= 65 && (a.d == 16 || a.d == 32 || a.d == 64) && (a.dv == 32 || a.dv == 64) &&
+  const bool resident = a.window <= 2 * BN + 1 && (a.d == 16 || a.d == 32 || a.d == 64) && (a.dv == 32 || a.dv == 64) &&
                         ((reinterpret_cast<uintptr_t>(a.q) | reinterpret_cast<uintptr_t>(a.k) |
                           reinterpret_cast<uintptr_t>(a.v) | reinterpret_cast<uintptr_t>(a.out)) & 15) == 0 &&
                         (size_t)a.N * (size_t)a.d * 2 < ((size_t)1 << 31) && (size_t)a.N * (size_t)a.dv * 2 < ((size_t)1 << 31);
