@@ -47,6 +47,19 @@
 
 namespace la {
 
+// Compute units of the current device (256 on MI355X when the query fails).
+int device_cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 namespace {
 
 struct ParallelParams {
@@ -693,18 +706,6 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   }
 }
 
-// Compute units of the current device (256 on MI355X when the query fails).
-int device_cu_count() {
-  static int cached[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
 
 // Packed path: pre-pass, column-sum scan, then the main kernel with 4 waves x 32 QT queries (8
 // waves x 32 queries at four waves per SIMD measured slower).

@@ -39,8 +39,12 @@ struct F32Params {
   int normalize, out_f32;
 };
 
-template <int KS, int MT, bool SLIDING>
-__global__ __launch_bounds__(256) void f32_attn_kernel(const F32Params p) {
+// SPLIT = 2 (BASED, small grids): two groups of four waves take the same 128 queries and every
+// other key block each, with a staging double buffer per group, and add their numerators and
+// row sums through LDS at the end, which halves the serial chain of key blocks of a query block.
+template <int KS, int MT, bool SLIDING, int SPLIT = 1>
+__global__ __launch_bounds__(256 * SPLIT) void f32_attn_kernel(const F32Params p) {
+  static_assert(SPLIT == 1 || (SPLIT == 2 && !SLIDING), "key split: BASED only");
   constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128, HALF = DK / 2;
   constexpr int KROW = DK + 4;
   constexpr int KCH = BNF * DK / 4;              // float4 chunks in a K block
@@ -48,10 +52,11 @@ __global__ __launch_bounds__(256) void f32_attn_kernel(const F32Params p) {
   constexpr int VGR = (DV / 4) * (BNF / 4);
   constexpr int VPT = (VGR + 255) / 256;
 
-  __shared__ __attribute__((aligned(16))) float Ks[2][BNF * KROW];
-  __shared__ __attribute__((aligned(16))) float VTs[2][DV * VROWF];
+  __shared__ __attribute__((aligned(16))) float Ks[SPLIT][2][BNF * KROW];
+  __shared__ __attribute__((aligned(16))) float VTs[SPLIT][2][DV * VROWF];
 
-  const int tid = threadIdx.x;
+  const int tid_all = threadIdx.x, tid = SPLIT == 2 ? tid_all & 255 : tid_all;   // thread within its group
+  const int grp = SPLIT == 2 ? __builtin_amdgcn_readfirstlane(tid_all >> 8) : 0;
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, n = lane & 31;
   const int N = p.N, d = p.d, dv = p.dv, W = p.window;
   int bh, qb;
@@ -118,7 +123,7 @@ __global__ __launch_bounds__(256) void f32_attn_kernel(const F32Params p) {
       const int c = tid + 256 * r;
       if (c < KCH) {
         const int key = c / (DK / 4), col = 4 * (c % (DK / 4));
-        *reinterpret_cast<f32x4*>(&Ks[s][key * KROW + col]) = kr[r];
+        *reinterpret_cast<f32x4*>(&Ks[grp][s][key * KROW + col]) = kr[r];
       }
     }
 #pragma unroll
@@ -128,28 +133,33 @@ __global__ __launch_bounds__(256) void f32_attn_kernel(const F32Params p) {
         const int g4 = g % (DV / 4), kg4 = g / (DV / 4);
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-          *reinterpret_cast<f32x4*>(&VTs[s][(4 * g4 + c) * VROWF + 4 * kg4]) =
+          *reinterpret_cast<f32x4*>(&VTs[grp][s][(4 * g4 + c) * VROWF + 4 * kg4]) =
               (f32x4){vr[r][0][c], vr[r][1][c], vr[r][2][c], vr[r][3][c]};
       }
     }
   };
 
-  load(jlo * BNF);
+  load((jlo + grp) * BNF);
   store(0);
   __syncthreads();
   const float inv_c = p.inv_c, inv_c2 = p.inv_c2, fscale = p.fscale, sl2 = p.scale_log2;
 
-  for (int j = jlo; j <= jhi; ++j) {
-    const int s = (j - jlo) & 1;
-    if (j < jhi) load((j + 1) * BNF);
-    if (wave_live) {
+  // group grp takes key blocks jlo + grp, jlo + grp + SPLIT, ...; every thread runs the same
+  // number of iterations (and barriers), a group past its last block idles in the last one
+  const int niter = (jhi - jlo + SPLIT) / SPLIT;
+  for (int it = 0; it < niter; ++it) {
+    const int j = jlo + SPLIT * it + grp;
+    const int s = it & 1;
+    const bool more = SPLIT == 1 ? j < jhi : it + 1 < niter;
+    if (more) load((j + SPLIT) * BNF);
+    if (wave_live && (SPLIT == 1 || j <= jhi)) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int kb = j * BNF + 32 * ks;
         if (kb > wq0 + 31) continue;
         if (SLIDING && kb + 31 < wq0 - W + 1) continue;
         f32x16 b = splat16(SLIDING ? 0.f : inv_c);
-        const float* kp = &Ks[s][(32 * ks + n) * KROW + HALF * h];
+        const float* kp = &Ks[grp][s][(32 * ks + n) * KROW + HALF * h];
 #pragma unroll
         for (int e = 0; e < HALF; ++e) b = mfma32x32x2_f32(kp[e], qf[e], b);
         float pv[16];
@@ -192,15 +202,37 @@ __global__ __launch_bounds__(256) void f32_attn_kernel(const F32Params p) {
         for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            const f32x4 vv = *reinterpret_cast<const f32x4*>(&VTs[s][(32 * mt + n) * VROWF + 32 * ks + 8 * g + 4 * h]);
+            const f32x4 vv = *reinterpret_cast<const f32x4*>(&VTs[grp][s][(32 * mt + n) * VROWF + 32 * ks + 8 * g + 4 * h]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[mt] = mfma32x32x2_f32(vv[e], pv[4 * g + e], acc[mt]);
           }
         }
       }
     }
-    if (j < jhi) store(s ^ 1);
+    if (more) store(s ^ 1);
     __syncthreads();
+  }
+
+  if (SPLIT == 2) {
+    // group 1 hands its numerators and row sums to group 0 through the (now free) stages
+    float* red = &VTs[0][0][0];
+    static_assert(SPLIT == 1 || 4 * (MT * 16 + 1) * 64 <= SPLIT * 2 * DV * VROWF, "reduction fits");
+    if (grp == 1 && wave_live) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) red[((w * MT + mt) * 16 + i) * 64 + lane] = acc[mt][i];
+      red[(4 * MT * 16 + w) * 64 + lane] = rsum;
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    if (wave_live) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[mt][i] += red[((w * MT + mt) * 16 + i) * 64 + lane];
+      rsum += red[(4 * MT * 16 + w) * 64 + lane];
+    }
   }
 
   if (!wave_live) return;
@@ -233,7 +265,15 @@ __global__ __launch_bounds__(256) void f32_attn_kernel(const F32Params p) {
 template <int KS, int MT, bool SL>
 int launch_f32(F32Params p, hipStream_t stream) {
   p.nqb = (p.N + 127) / 128;
-  hipLaunchKernelGGL((f32_attn_kernel<KS, MT, SL>), dim3((unsigned)(p.nqb * p.BH)), dim3(256), 0, stream, p);
+  const dim3 grid((unsigned)(p.nqb * p.BH));
+  if constexpr (!SL && KS == 1 && MT <= 2) {
+    // fewer query blocks than CUs: split every query block's keys over two wave groups
+    if ((long long)p.nqb * p.BH < device_cu_count()) {
+      hipLaunchKernelGGL((f32_attn_kernel<KS, MT, SL, 2>), grid, dim3(512), 0, stream, p);
+      return (int)hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((f32_attn_kernel<KS, MT, SL>), grid, dim3(256), 0, stream, p);
   return (int)hipGetLastError();
 }
 

@@ -88,6 +88,7 @@ int launch_sliding_window(const SlidingArgs& a, hipStream_t stream);
 size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk);
 int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream);
 int launch_feature_map(const FeatureMapArgs& a, hipStream_t stream);
+int device_cu_count();   // compute units of the current device (256 when the query fails)
 bool identity_shape(int d, int dv);
 size_t identity_workspace_bytes(int BH, int N, int d, int dv);
 int launch_identity(const IdentityArgs& a, hipStream_t stream);
