@@ -67,7 +67,7 @@ def parse():
                     help="only time the full BASED layer (linear attention + sliding-window softmax, the sum "
                          "taken in the sliding kernel's store) against the two branches run and added apart")
     ap.add_argument("--decode", action="store_true",
-                    help="only time one decode step (la_based_decode_step, d16 dv64) on the exported state")
+                    help="only time one decode step (la_based_decode_step{,_ws}, d16 dv64) on the exported state")
     ap.add_argument("--identity", action="store_true",
                     help="only time the identity-map linear attention numerator (la_identity_linear_fwd) at "
                          "B2 H16 N8192 d16 dv64 bf16 against its HBM roofline")
@@ -284,14 +284,18 @@ def _lib_handle():
 
 
 def decode_bench(steps, warmup, device):
-    """ms per decode step (one token per head) at a serving batch and at the headline's heads;
-    HBM-bound: the fp32 state is read and written once, 2 x 4 F (dv + 1) bytes per head."""
+    """ms per decode step (one token per head) at serving batches and at the headline's heads;
+    HBM-bound: the fp32 state is read and written once, 2 x 4 F (dv + 1) bytes per head.
+    `ms`: la_based_decode_step_ws (a head's state rows split over several work-groups when the
+    batch is small), `ms_one_group`: la_based_decode_step (one work-group per head),
+    `ms_graph`: 16 steps of the Python wrapper captured in one HIP graph and replayed (no host
+    launch cost), `ms_python_wrapper`: the wrapper called eagerly."""
     import torch
 
     import kernels as K
 
     rows = []
-    for B, H in [(2, 16), (64, 16)]:
+    for B, H in [(2, 16), (8, 16), (64, 16)]:
         d, dv, F = 16, 64, K.feature_dim(16)
         g = torch.Generator(device=device).manual_seed(3)
         q, k, v = (torch.randn(B, H, n, generator=g, device=device).bfloat16() * 0.5 for n in (d, d, dv))
@@ -299,18 +303,40 @@ def decode_bench(steps, warmup, device):
         out = torch.empty(B, H, dv, dtype=torch.bfloat16, device=device)
         L = _lib_handle()
         stream = torch.cuda.current_stream(device).cuda_stream
+        need = int(L.la_based_decode_workspace_bytes(B, H, d, dv))
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
 
-        def abi():
+        def abi_ws():
+            rc = L.la_based_decode_step_ws(q.data_ptr(), k.data_ptr(), v.data_ptr(), 1, st.data_ptr(), out.data_ptr(),
+                                           1, B, H, d, dv, 1e-6, 1, ws.data_ptr(), need, stream)
+            if rc != 0:
+                raise RuntimeError(f"la_based_decode_step_ws: {rc}")
+
+        def abi_one():
             rc = L.la_based_decode_step(q.data_ptr(), k.data_ptr(), v.data_ptr(), 1, st.data_ptr(), out.data_ptr(), 1,
                                         B, H, d, dv, 1e-6, 1, stream)
             if rc != 0:
                 raise RuntimeError(f"la_based_decode_step: {rc}")
 
-        ms = time_calls([abi], steps, warmup)
+        ms = time_calls([abi_ws], steps, warmup)
+        ms_one = time_calls([abi_one], steps, warmup)
         ms_py = time_calls([lambda: K.based_decode_step(q, k, v, st)], steps, warmup)
+        graph_steps = 16
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            K.based_decode_step(q, k, v, st)
+        torch.cuda.current_stream(device).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(graph_steps):
+                K.based_decode_step(q, k, v, st)
+        ms_graph = time_calls([graph.replay], max(1, steps // graph_steps), 2) / graph_steps
         nbytes = 2 * B * H * F * (dv + 1) * 4
-        rows.append({"B": B, "H": H, "d": d, "dv": dv, "ms": round(ms, 5), "ms_python_wrapper": round(ms_py, 5),
-                     "state_bytes_moved": nbytes, "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+        rows.append({"B": B, "H": H, "d": d, "dv": dv, "workspace_bytes": need, "ms": round(ms, 5),
+                     "ms_one_group": round(ms_one, 5), "ms_graph": round(ms_graph, 5),
+                     "ms_python_wrapper": round(ms_py, 5), "state_bytes_moved": nbytes,
+                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)})
     return {"decode": rows}
 
 

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 5
+#define LA_ABI_VERSION 6
 
 /* element types */
 #define LA_F32 0
@@ -163,6 +163,22 @@ int la_sliding_window_fwd_add(const void* q, const void* k, const void* v, int i
 int la_based_decode_step(const void* q, const void* k, const void* v, int in_dtype,
                          float* state, void* out, int out_dtype, int B, int H, int d, int dv,
                          float eps, int normalize, void* hip_stream);
+
+/*
+ * la_based_decode_step with a caller-owned workspace (no reference counterpart, like
+ * la_based_decode_step).  The workspace lets a small batch split every head's state rows over
+ * several work-groups, whose partial column sums are then added in a fixed order
+ * (deterministic, but rounded differently from la_based_decode_step).
+ * la_based_decode_workspace_bytes gives the size: 0 when one work-group per head already
+ * fills the device, or for shapes outside the limits.  The workspace can then be NULL, and the
+ * call is la_based_decode_step.  Otherwise it holds B*H*R*(dv+1) floats for R row groups per
+ * head.  It must be 4-byte aligned and must not overlap state, q, k, v or out.
+ */
+size_t la_based_decode_workspace_bytes(int B, int H, int d, int dv);
+int la_based_decode_step_ws(const void* q, const void* k, const void* v, int in_dtype,
+                            float* state, void* out, int out_dtype, int B, int H, int d, int dv,
+                            float eps, int normalize, void* workspace, size_t workspace_bytes,
+                            void* hip_stream);
 
 /*
  * Causal linear attention with the identity feature map, numerator only:

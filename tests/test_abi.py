@@ -27,7 +27,8 @@ def test_header_declares_expected_entry_points():
     assert _declared() == sorted([
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
         "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_fwd", "la_based_chunked_fwd_continue", "la_sliding_window_fwd",
-        "la_sliding_window_fwd_add", "la_based_decode_step", "la_identity_workspace_bytes", "la_identity_linear_fwd",
+        "la_sliding_window_fwd_add", "la_based_decode_step", "la_based_decode_workspace_bytes",
+        "la_based_decode_step_ws", "la_identity_workspace_bytes", "la_identity_linear_fwd",
         "la_taylor_feature_map"])
 
 
@@ -39,7 +40,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib()
-    assert lib.la_abi_version() == 5
+    assert lib.la_abi_version() == 6
     for code in range(-9, 1):
         s = lib.la_status_string(code).decode()
         assert s and s != "unknown status"
@@ -136,6 +137,36 @@ def test_decode_argument_errors():
     assert call(10, 129) == -5                        # dv
     assert call(11, -1.0) == -4                       # eps
     assert call(3, 5) == -3                           # dtype
+    assert call(7, 0) == 0                            # B = 0: nothing to launch
+
+
+def test_decode_workspace_sizes_and_errors():
+    lib = _lib()
+    ws = lib.la_based_decode_workspace_bytes
+    # B*H heads split into R row groups of the F = 153 state rows (d = 16) until about 1024
+    # work-groups launch, at least 8 rows each: R = 20 for 2 heads, 8 for 128, 2 for 640, 1 for
+    # 1024 (no workspace); one fp32 partial sum per group and column (dv + 1 columns).
+    assert ws(1, 2, 16, 64) == 2 * 20 * 65 * 4
+    assert ws(8, 16, 16, 64) == 128 * 8 * 65 * 4
+    assert ws(40, 16, 16, 64) == 640 * 2 * 65 * 4
+    assert ws(64, 16, 16, 64) == 0
+    assert ws(1, 1, 64, 128) == 269 * 129 * 4        # F = 2145 in groups of 8 rows
+    assert ws(1, 1, 65, 8) == 0 and ws(1, 1, 16, 129) == 0 and ws(-1, 1, 16, 8) == 0
+    f = lib.la_based_decode_step_ws
+    need = ws(1, 2, 16, 64)
+    ok = [P, P, P, 1, P, P, 1, 1, 2, 16, 64, 1e-6, 1, P, need, None]
+
+    def call(i, x):
+        a = list(ok)
+        a[i] = x
+        return f(*a)
+
+    assert call(13, None) == -6                       # workspace needed
+    assert call(14, need - 1) == -6                   # workspace too small
+    assert call(13, ctypes.c_void_p((1 << 20) + 2)) == -8   # workspace not 4-byte aligned
+    assert call(4, None) == -1                        # state
+    assert call(9, 65) == -5                          # d
+    assert call(11, float("nan")) == -4               # eps
     assert call(7, 0) == 0                            # B = 0: nothing to launch
 
 

@@ -77,3 +77,38 @@ def test_decode_errors():
     q3 = torch.zeros(1, 2, 65, device="cuda", dtype=torch.bfloat16)
     with pytest.raises(RuntimeError):
         K.based_decode_step(q3, q3, v[:, :, 0], torch.zeros(1, 2, K.feature_dim(65), 9, device="cuda"))   # d > 64
+
+
+@pytest.mark.parametrize("B,H,d,dv", [(1, 1, 16, 64), (2, 16, 16, 64), (40, 16, 16, 64), (1, 3, 64, 128),
+                                      (3, 5, 7, 5), (1, 1, 1, 1)])
+def test_split_rows_match_one_group_per_head(B, H, d, dv):
+    """la_based_decode_step_ws (state rows split over work-groups when the batch is small) against
+    la_based_decode_step (one work-group per head), through the C ABI: the updated states are
+    bit-identical (the same fma per element) and the outputs agree to fp32 rounding (the partial
+    column sums are added in another order: the fp32 bar); twice in a row on the same workspace."""
+    K = _kernels()
+    from kernels import _lib
+    L = _lib.lib()
+    F = K.feature_dim(d)
+    need = int(L.la_based_decode_workspace_bytes(B, H, d, dv))
+    assert (need > 0) == (B * H < 1024 and F > 8)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+    # the state of 8 earlier tokens (every token adds 1 + s + s^2/2 >= 1/2 to a denominator)
+    _, k0, v0 = rand_qkv(B, H, 8, d, dv, seed=B * 1000 + d * 10 + dv, dtype=torch.float32, scale_qk=0.5)
+    st = _state_closed_form(k0, v0).float().cuda()
+    assert st.shape == (B, H, F, dv + 1)
+    st_one, st_split = st.clone(), st.clone()
+    for step in range(2):
+        q, k, v = to_dev(*rand_qkv(B, H, 1, d, dv, seed=step + 7 * d, dtype=torch.float32, scale_qk=0.5))
+        y_one = torch.empty(B, H, dv, device="cuda")
+        y_split = torch.full((B, H, dv), float("nan"), device="cuda")
+        args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), 0)
+        rc = L.la_based_decode_step(*args, _lib.ptr(st_one), _lib.ptr(y_one), 0, B, H, d, dv, 1e-6, 1,
+                                    _lib.stream_of(q))
+        assert rc == 0
+        rc = L.la_based_decode_step_ws(*args, _lib.ptr(st_split), _lib.ptr(y_split), 0, B, H, d, dv, 1e-6, 1,
+                                       _lib.ptr(ws), need, _lib.stream_of(q))
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert torch.equal(st_one, st_split)
+        assert err(y_split, y_one.cpu()) < 1e-4   # the fp32 bar (2145-term sums at d = 64)

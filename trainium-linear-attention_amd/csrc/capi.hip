@@ -229,8 +229,9 @@ int la_identity_linear_fwd(const void* q, const void* k, const void* v, int in_d
   return la::launch_identity(a, static_cast<hipStream_t>(hip_stream));
 }
 
-int la_based_decode_step(const void* q, const void* k, const void* v, int in_dtype, float* state, void* out,
-                         int out_dtype, int B, int H, int d, int dv, float eps, int normalize, void* hip_stream) {
+static int decode_common(const void* q, const void* k, const void* v, int in_dtype, float* state, void* out,
+                         int out_dtype, int B, int H, int d, int dv, float eps, int normalize, bool with_ws,
+                         void* workspace, size_t workspace_bytes, void* hip_stream) {
   int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, 1, d, dv);
   if (rc != LA_OK) return rc;
   if (!la::decode_shape(d, dv)) return LA_ERR_UNSUPPORTED_DIM;
@@ -239,6 +240,12 @@ int la_based_decode_step(const void* q, const void* k, const void* v, int in_dty
   if (state == nullptr) return LA_ERR_NULL_POINTER;
   if (reinterpret_cast<uintptr_t>(state) & 3) return LA_ERR_BAD_ALIGNMENT;
   la::DecodeArgs a{};
+  if (with_ws) {
+    const size_t need = la::decode_workspace_bytes((long long)B * H, d, dv);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
+    if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 3)) return LA_ERR_BAD_ALIGNMENT;
+    a.workspace = need > 0 ? workspace : nullptr;
+  }
   a.q = q;
   a.k = k;
   a.v = v;
@@ -252,6 +259,24 @@ int la_based_decode_step(const void* q, const void* k, const void* v, int in_dty
   a.in_f32 = in_dtype == LA_F32;
   a.out_f32 = out_dtype == LA_F32;
   return la::launch_decode_step(a, static_cast<hipStream_t>(hip_stream));
+}
+
+int la_based_decode_step(const void* q, const void* k, const void* v, int in_dtype, float* state, void* out,
+                         int out_dtype, int B, int H, int d, int dv, float eps, int normalize, void* hip_stream) {
+  return decode_common(q, k, v, in_dtype, state, out, out_dtype, B, H, d, dv, eps, normalize, false, nullptr, 0,
+                       hip_stream);
+}
+
+size_t la_based_decode_workspace_bytes(int B, int H, int d, int dv) {
+  if (B < 0 || H < 0 || !la::decode_shape(d, dv)) return 0;
+  return la::decode_workspace_bytes((long long)B * H, d, dv);
+}
+
+int la_based_decode_step_ws(const void* q, const void* k, const void* v, int in_dtype, float* state, void* out,
+                            int out_dtype, int B, int H, int d, int dv, float eps, int normalize, void* workspace,
+                            size_t workspace_bytes, void* hip_stream) {
+  return decode_common(q, k, v, in_dtype, state, out, out_dtype, B, H, d, dv, eps, normalize, true, workspace,
+                       workspace_bytes, hip_stream);
 }
 
 static int sliding_common(const void* q, const void* k, const void* v, int in_dtype, bool with_addend,

@@ -10,11 +10,18 @@
 // token (its intra-chunk term phi(q).phi(k) v is the contribution of the token's own row of the
 // update).  The reference has no decode path; this continues a prefill that exported its state.
 //
-// One work-group per head: phi(q) and phi(k) go to LDS, then the head's state is swept linearly
+// A head's F state rows are split into R groups of consecutive rows, one work-group each: phi(q)
+// and phi(k) of the group's rows go to LDS, then the group's rows are swept linearly
 // (coalesced) in tiles of 32 rows, each element updated in place, and the column sums of phi(q)
-// times the updated state are taken per tile through LDS in row order (deterministic).
-// HBM-bound: the state is read and written once (4 F (dv + 1) bytes each way per head).
+// times the updated state are taken per tile through LDS in row order.  With R = 1 the
+// work-group normalises and stores the output itself; with R > 1 it stores its column sums to
+// a workspace and a combine kernel adds the R partial sums of every column in group order
+// (deterministic) and normalises.  R is chosen so that small batches still launch enough
+// work-groups to cover the chip.  HBM-bound: the state is read and written once
+// (4 F (dv + 1) bytes each way per head).
 #include <math.h>
+
+#include <algorithm>
 
 #include "la_common.hpp"
 #include "la_internal.hpp"
@@ -39,6 +46,10 @@ constexpr int kDecMaxD = 64;
 constexpr int kDecMaxC = 129;   // dv + 1 for dv <= 128
 constexpr int kDecMaxF = 1 + kDecMaxD + kDecMaxD * (kDecMaxD + 1) / 2;
 constexpr int kDecRows = 32;    // state rows per reduction tile
+constexpr int kDecMinRows = 8;  // fewest state rows per work-group when a head is split
+#ifndef LA_DECODE_TARGET_WGS
+#define LA_DECODE_TARGET_WGS 1024   // split heads until about this many work-groups launch
+#endif
 
 __device__ __forceinline__ float load_elem(const void* base, size_t i, bool f32) {
   return f32 ? static_cast<const float*>(base)[i] : bf16_bits_to_f32(static_cast<const uint16_t*>(base)[i]);
@@ -60,12 +71,16 @@ __device__ __forceinline__ float feature(const float* x, int f, int d, float r4,
   return x[i] * x[i + 1 + t] * rd;
 }
 
-__global__ __launch_bounds__(kDecThreads) void based_decode_kernel(const DecodeParams p) {
+// Rows [g RW, min(F, (g + 1) RW)) of head bh = blockIdx.x, g = blockIdx.y.  PARTIAL: store
+// the group's column sums to part[(bh R + g) C + c]; else (R = 1) normalise and store the output.
+template <bool PARTIAL>
+__global__ __launch_bounds__(kDecThreads) void based_decode_kernel(const DecodeParams p, int RW, float* part) {
   __shared__ float xq[kDecMaxD], xk[kDecMaxD], vv[kDecMaxC];
   __shared__ float phq[kDecMaxF], phk[kDecMaxF];
   __shared__ float tile[kDecRows * kDecMaxC];
-  const int bh = blockIdx.x, tid = threadIdx.x;
+  const int bh = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
   const int d = p.d, dv = p.dv, F = p.F, C = dv + 1;
+  const int rb = g * RW, re = min(F, rb + RW);
   if (tid < d) {
     xq[tid] = load_elem(p.q, (size_t)bh * d + tid, p.in_f32);
     xk[tid] = load_elem(p.k, (size_t)bh * d + tid, p.in_f32);
@@ -74,32 +89,70 @@ __global__ __launch_bounds__(kDecThreads) void based_decode_kernel(const DecodeP
   if (tid == 0) vv[dv] = 1.f;
   __syncthreads();
   const float rd = 1.0f / sqrtf((float)d), r4 = sqrtf(rd), rsq = rd * 0.70710678118654752f;
-  for (int f = tid; f < F; f += kDecThreads) {
-    phq[f] = feature(xq, f, d, r4, rsq, rd);
-    phk[f] = feature(xk, f, d, r4, rsq, rd);
+  for (int f = rb + tid; f < re; f += kDecThreads) {
+    phq[f - rb] = feature(xq, f, d, r4, rsq, rd);
+    phk[f - rb] = feature(xk, f, d, r4, rsq, rd);
   }
   __syncthreads();
 
-  // The state sweeps linearly (coalesced) in tiles of kDecRows rows: every element is updated
-  // in place and its phi(q)-weighted value parked in LDS, then thread c < C adds the tile's
-  // column c in row order.
+  // The rows sweep linearly (coalesced) in tiles of kDecRows rows: every element is updated in
+  // place and its phi(q)-weighted value parked in LDS, then thread c < C adds the tile's column
+  // c in row order.
   float* __restrict__ st = p.state + (size_t)bh * F * C;
   float colsum = 0.f;
-  for (int r0 = 0; r0 < F; r0 += kDecRows) {
-    const int ne = min(kDecRows, F - r0) * C;
+  for (int r0 = rb; r0 < re; r0 += kDecRows) {
+    const int ne = min(kDecRows, re - r0) * C;
     float* __restrict__ base = st + (size_t)r0 * C;
+    const float* pk = phk + (r0 - rb);
+    const float* pq = phq + (r0 - rb);
     for (int e = tid; e < ne; e += kDecThreads) {
       const int fr = e / C, c = e - fr * C;
-      const float s = __builtin_fmaf(phk[r0 + fr], vv[c], base[e]);
+      const float s = __builtin_fmaf(pk[fr], vv[c], base[e]);
       base[e] = s;
-      tile[e] = phq[r0 + fr] * s;
+      tile[e] = pq[fr] * s;
     }
     __syncthreads();
     if (tid < C)
       for (int e = tid; e < ne; e += C) colsum += tile[e];
     __syncthreads();
   }
+  if (PARTIAL) {
+    if (tid < C) part[((size_t)bh * gridDim.y + g) * C + tid] = colsum;
+    return;
+  }
   __shared__ float den;
+  if (tid == dv) den = colsum;
+  __syncthreads();
+  if (tid < dv) {
+    const float y = p.normalize ? colsum / (den + p.eps) : colsum;
+    const size_t o = (size_t)bh * dv + tid;
+    if (p.out_f32)
+      static_cast<float*>(p.out)[o] = y;
+    else
+      static_cast<uint16_t*>(p.out)[o] = f32_to_bf16_bits(y);
+  }
+}
+
+// Head bh = blockIdx.x: column c = sum over groups g = 0 .. R-1 (in that order) of
+// part[(bh R + g) C + c], then the output as in the single-group kernel.
+__global__ __launch_bounds__(kDecThreads) void decode_combine_kernel(const DecodeParams p, int R,
+                                                                     const float* __restrict__ part) {
+  __shared__ float den;
+  const int bh = blockIdx.x, tid = threadIdx.x, dv = p.dv, C = dv + 1;
+  float colsum = 0.f;
+  if (tid < C) {
+    // eight loads in flight at a time; the additions keep group order
+    const float* src = part + (size_t)bh * R * C + tid;
+    int g = 0;
+    for (; g + 8 <= R; g += 8) {
+      float t[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) t[i] = src[(size_t)(g + i) * C];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) colsum += t[i];
+    }
+    for (; g < R; ++g) colsum += src[(size_t)g * C];
+  }
   if (tid == dv) den = colsum;
   __syncthreads();
   if (tid < dv) {
@@ -116,6 +169,22 @@ __global__ __launch_bounds__(kDecThreads) void based_decode_kernel(const DecodeP
 
 bool decode_shape(int d, int dv) { return d >= 1 && d <= kDecMaxD && dv >= 1 && dv + 1 <= kDecMaxC; }
 
+// Row groups per head: enough work-groups for the chip, at least kDecMinRows rows each; RW =
+// rows per group (the last group may have fewer).
+static void decode_groups(long long BH, int d, int& R, int& RW) {
+  const int F = 1 + d + d * (d + 1) / 2;
+  long long r = (LA_DECODE_TARGET_WGS + BH - 1) / BH;
+  r = std::max(1LL, std::min(r, (long long)((F + kDecMinRows - 1) / kDecMinRows)));
+  RW = (int)((F + r - 1) / r);
+  R = (F + RW - 1) / RW;
+}
+
+size_t decode_workspace_bytes(long long BH, int d, int dv) {
+  int R, RW;
+  decode_groups(BH, d, R, RW);
+  return R > 1 ? (size_t)BH * R * (dv + 1) * sizeof(float) : 0;
+}
+
 int launch_decode_step(const DecodeArgs& a, hipStream_t stream) {
   DecodeParams p{};
   p.q = a.q;
@@ -131,7 +200,18 @@ int launch_decode_step(const DecodeArgs& a, hipStream_t stream) {
   p.normalize = a.normalize ? 1 : 0;
   p.in_f32 = a.in_f32 ? 1 : 0;
   p.out_f32 = a.out_f32 ? 1 : 0;
-  hipLaunchKernelGGL(based_decode_kernel, dim3((unsigned)a.BH), dim3(kDecThreads), 0, stream, p);
+  int R = 1, RW = p.F;
+  if (a.workspace != nullptr) decode_groups(a.BH, a.d, R, RW);
+  if (R == 1) {
+    hipLaunchKernelGGL(based_decode_kernel<false>, dim3((unsigned)a.BH, 1), dim3(kDecThreads), 0, stream, p, RW,
+                       static_cast<float*>(nullptr));
+  } else {
+    float* part = static_cast<float*>(a.workspace);
+    hipLaunchKernelGGL(based_decode_kernel<true>, dim3((unsigned)a.BH, (unsigned)R), dim3(kDecThreads), 0, stream,
+                       p, RW, part);
+    hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)a.BH), dim3(kDecThreads), 0, stream, p, R,
+                       static_cast<const float*>(part));
+  }
   return (int)hipGetLastError();
 }
 

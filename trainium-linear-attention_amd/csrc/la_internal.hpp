@@ -67,6 +67,7 @@ struct DecodeArgs {
   const void* v;       // (BH, dv)
   float* state;        // (BH, F, dv + 1) fp32, updated in place
   void* out;           // (BH, dv)
+  void* workspace;     // decode_workspace_bytes(BH, d, dv) bytes, or null: one work-group per head
   int BH, d, dv;
   float eps;
   bool normalize, in_f32, out_f32;
@@ -94,6 +95,7 @@ size_t identity_workspace_bytes(int BH, int N, int d, int dv);
 int launch_identity(const IdentityArgs& a, hipStream_t stream);
 bool decode_shape(int d, int dv);
 int launch_decode_step(const DecodeArgs& a, hipStream_t stream);
+size_t decode_workspace_bytes(long long BH, int d, int dv);
 
 // Work-group order for causal query blocks: heaviest (last) blocks first over all the heads an
 // XCD owns, so that greedy dispatch as slots free up balances the causal triangle (a head-major

@@ -52,13 +52,16 @@ _SIGNATURES = {
                                                _c_size, _c_void, ctypes.c_longlong, _c_void, _c_void]),
     "la_based_decode_step": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int, _c_int,
                                       _c_int, _c_int, _c_float, _c_int, _c_void]),
+    "la_based_decode_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "la_based_decode_step_ws": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int,
+                                         _c_int, _c_int, _c_int, _c_float, _c_int, _c_void, _c_size, _c_void]),
     "la_identity_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "la_identity_linear_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int, _c_int,
                                         _c_int, _c_int, _c_float, _c_void, _c_size, _c_void]),
     "la_taylor_feature_map": (_c_int, [_c_void, _c_int, _c_void, _c_int, ctypes.c_longlong, _c_int, _c_void]),
 }
 
-EXPECTED_ABI = 5
+EXPECTED_ABI = 6
 
 
 class BasedLAError(RuntimeError):

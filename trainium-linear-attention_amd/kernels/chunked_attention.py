@@ -116,8 +116,10 @@ def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, 
 
 def based_decode_step(q, k, v, state, eps=1e-6, normalize=True):
     """One decode step on an exported state (``based_chunked(..., return_state=True)``) through
-    ``la_based_decode_step``: ``state`` (b, h, F, dv + 1) fp32 = [S | z] is updated in place with
-    the new token, ``[S | z] += phi(k) [v | 1]``, and the token's output is returned,
+    ``la_based_decode_step_ws`` (small batches split every head's state rows over several
+    work-groups, with a workspace allocated here): ``state`` (b, h, F, dv + 1) fp32 = [S | z]
+    is updated in place with the new token, ``[S | z] += phi(k) [v | 1]``, and the token's
+    output is returned,
     ``phi(q) S / (phi(q) z + eps)`` (the numerator with ``normalize=False``), in q.dtype.
 
     q, k: (b, h, d) or (b, h, 1, d); v: (b, h, dv) or (b, h, 1, dv) -- one token per head.
@@ -143,10 +145,14 @@ def based_decode_step(q, k, v, state, eps=1e-6, normalize=True):
     kdt = q.dtype if q.dtype in (torch.float32, torch.bfloat16) else torch.float32
     qc, kc, vc = (_as_kernel_input(x, cdt) for x in (q, k, v))
     out = torch.empty(b, h, dv, dtype=kdt, device=q.device)
-    rc = _lib.lib().la_based_decode_step(
+    L = _lib.lib()
+    ws_bytes = int(L.la_based_decode_workspace_bytes(b, h, d, dv))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes > 0 else None
+    rc = L.la_based_decode_step_ws(
         _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.dtype_code(cdt), _lib.ptr(state), _lib.ptr(out),
-        _lib.dtype_code(kdt), b, h, d, dv, float(eps), 1 if normalize else 0, _lib.stream_of(q))
-    _lib.check(rc, "la_based_decode_step")
+        _lib.dtype_code(kdt), b, h, d, dv, float(eps), 1 if normalize else 0, _lib.ptr(ws), ws_bytes,
+        _lib.stream_of(q))
+    _lib.check(rc, "la_based_decode_step_ws")
     if out.dtype != q.dtype:
         out = out.to(q.dtype)
     return out.unsqueeze(2) if squeeze else out
