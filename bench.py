@@ -286,8 +286,10 @@ def _lib_handle():
 def decode_bench(steps, warmup, device):
     """ms per decode step (one token per head) at serving batches and at the headline's heads;
     HBM-bound: the fp32 state is read and written once, 2 x 4 F (dv + 1) bytes per head.
-    `ms`: la_based_decode_step_ws (a head's state rows split over several work-groups when the
-    batch is small), `ms_one_group`: la_based_decode_step (one work-group per head),
+    `ms`: la_based_decode_step_ws, `ms_one_group`: la_based_decode_step.  A state of at most
+    10240 floats per head (d16 dv64) is held in LDS by one 1024-thread work-group in both;
+    larger ones (dv128) go through 256-thread work-groups, whose rows the workspace entry point
+    splits over several work-groups when the batch is small,
     `ms_graph`: 16 steps of the Python wrapper captured in one HIP graph and replayed (no host
     launch cost), `ms_python_wrapper`: the wrapper called eagerly."""
     import torch
@@ -295,8 +297,8 @@ def decode_bench(steps, warmup, device):
     import kernels as K
 
     rows = []
-    for B, H in [(2, 16), (8, 16), (64, 16)]:
-        d, dv, F = 16, 64, K.feature_dim(16)
+    for B, H, dv in [(2, 16, 64), (8, 16, 64), (64, 16, 64), (2, 16, 128), (64, 16, 128)]:
+        d, F = 16, K.feature_dim(16)
         g = torch.Generator(device=device).manual_seed(3)
         q, k, v = (torch.randn(B, H, n, generator=g, device=device).bfloat16() * 0.5 for n in (d, d, dv))
         st = torch.zeros(B, H, F, dv + 1, device=device)

@@ -169,9 +169,10 @@ int la_based_decode_step(const void* q, const void* k, const void* v, int in_dty
  * la_based_decode_step).  The workspace lets a small batch split every head's state rows over
  * several work-groups, whose partial column sums are then added in a fixed order
  * (deterministic, but rounded differently from la_based_decode_step).
- * la_based_decode_workspace_bytes gives the size: 0 when one work-group per head already
- * fills the device, or for shapes outside the limits.  The workspace can then be NULL, and the
- * call is la_based_decode_step.  Otherwise it holds B*H*R*(dv+1) floats for R row groups per
+ * la_based_decode_workspace_bytes gives the size.  It is 0 when a head's state fits in LDS
+ * (F*(dv+1) <= 10240 floats), when one work-group per head already fills the device, or for
+ * shapes outside the limits; the workspace can then be NULL, and the call is
+ * la_based_decode_step.  Otherwise it holds B*H*R*(dv+1) floats for R row groups per
  * head.  It must be 4-byte aligned and must not overlap state, q, k, v or out.
  */
 size_t la_based_decode_workspace_bytes(int B, int H, int d, int dv);

@@ -143,18 +143,22 @@ def test_decode_argument_errors():
 def test_decode_workspace_sizes_and_errors():
     lib = _lib()
     ws = lib.la_based_decode_workspace_bytes
-    # B*H heads split into R row groups of the F = 153 state rows (d = 16) until about 1024
-    # work-groups launch, at least 8 rows each: R = 20 for 2 heads, 8 for 128, 2 for 640, 1 for
-    # 1024 (no workspace); one fp32 partial sum per group and column (dv + 1 columns).
-    assert ws(1, 2, 16, 64) == 2 * 20 * 65 * 4
-    assert ws(8, 16, 16, 64) == 128 * 8 * 65 * 4
-    assert ws(40, 16, 16, 64) == 640 * 2 * 65 * 4
-    assert ws(64, 16, 16, 64) == 0
+    # A head's state of F (dv + 1) <= 10240 floats is held in LDS by one work-group: no
+    # workspace (d = 16: F = 153, so dv <= 65).  Larger states: B*H heads split into R row
+    # groups of the F rows until about 1024 work-groups launch, at least 8 rows each: R = 20 for
+    # 2 heads, 8 for 128, 2 for 640, 1 for 1024 (no workspace); one fp32 partial sum per group
+    # and column (dv + 1 columns).
+    assert ws(1, 2, 16, 64) == 0 and ws(1, 1, 16, 65) == 0 and ws(1, 1, 4, 128) == 0
+    assert ws(1, 1, 16, 66) == 20 * 67 * 4
+    assert ws(1, 2, 16, 128) == 2 * 20 * 129 * 4
+    assert ws(8, 16, 16, 128) == 128 * 8 * 129 * 4
+    assert ws(40, 16, 16, 128) == 640 * 2 * 129 * 4
+    assert ws(64, 16, 16, 128) == 0
     assert ws(1, 1, 64, 128) == 269 * 129 * 4        # F = 2145 in groups of 8 rows
     assert ws(1, 1, 65, 8) == 0 and ws(1, 1, 16, 129) == 0 and ws(-1, 1, 16, 8) == 0
     f = lib.la_based_decode_step_ws
-    need = ws(1, 2, 16, 64)
-    ok = [P, P, P, 1, P, P, 1, 1, 2, 16, 64, 1e-6, 1, P, need, None]
+    need = ws(1, 2, 16, 128)
+    ok = [P, P, P, 1, P, P, 1, 1, 2, 16, 128, 1e-6, 1, P, need, None]
 
     def call(i, x):
         a = list(ok)

@@ -79,11 +79,12 @@ def test_decode_errors():
         K.based_decode_step(q3, q3, v[:, :, 0], torch.zeros(1, 2, K.feature_dim(65), 9, device="cuda"))   # d > 64
 
 
-@pytest.mark.parametrize("B,H,d,dv", [(1, 1, 16, 64), (2, 16, 16, 64), (40, 16, 16, 64), (1, 3, 64, 128),
-                                      (3, 5, 7, 5), (1, 1, 1, 1)])
+@pytest.mark.parametrize("B,H,d,dv", [(2, 16, 16, 128), (40, 16, 16, 128), (1, 1, 16, 66), (1, 3, 64, 128),
+                                      (8, 16, 32, 64), (2, 16, 16, 64), (64, 16, 16, 64), (3, 5, 7, 5),
+                                      (1, 1, 1, 1)])
 def test_split_rows_match_one_group_per_head(B, H, d, dv):
-    """la_based_decode_step_ws (state rows split over work-groups when the batch is small) against
-    la_based_decode_step (one work-group per head), through the C ABI: the updated states are
+    """la_based_decode_step_ws (state rows split over work-groups when the batch is small and the
+    state does not fit in LDS) against la_based_decode_step, through the C ABI: the updated states are
     bit-identical (the same fma per element) and the outputs agree to fp32 rounding (the partial
     column sums are added in another order: the fp32 bar); twice in a row on the same workspace."""
     K = _kernels()
@@ -91,7 +92,7 @@ def test_split_rows_match_one_group_per_head(B, H, d, dv):
     L = _lib.lib()
     F = K.feature_dim(d)
     need = int(L.la_based_decode_workspace_bytes(B, H, d, dv))
-    assert (need > 0) == (B * H < 1024 and F > 8)
+    assert (need > 0) == (B * H < 1024 and F > 8 and F * (dv + 1) > 10240)
     ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
     # the state of 8 earlier tokens (every token adds 1 + s + s^2/2 >= 1/2 to a denominator)
     _, k0, v0 = rand_qkv(B, H, 8, d, dv, seed=B * 1000 + d * 10 + dv, dtype=torch.float32, scale_qk=0.5)

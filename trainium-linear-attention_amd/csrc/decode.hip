@@ -10,7 +10,9 @@
 // token (its intra-chunk term phi(q).phi(k) v is the contribution of the token's own row of the
 // update).  The reference has no decode path; this continues a prefill that exported its state.
 //
-// A head's F state rows are split into R groups of consecutive rows, one work-group each: phi(q)
+// A head whose state fits in LDS (F (dv + 1) <= 10240 floats) runs in one 1024-thread
+// work-group that loads the whole state at once (based_decode_wide_kernel).  Otherwise a
+// head's F state rows are split into R groups of consecutive rows, one work-group each: phi(q)
 // and phi(k) of the group's rows go to LDS, then the group's rows are swept linearly
 // (coalesced) in tiles of 32 rows, each element updated in place, and the column sums of phi(q)
 // times the updated state are taken per tile through LDS in row order.  With R = 1 the
@@ -47,6 +49,9 @@ constexpr int kDecMaxC = 129;   // dv + 1 for dv <= 128
 constexpr int kDecMaxF = 1 + kDecMaxD + kDecMaxD * (kDecMaxD + 1) / 2;
 constexpr int kDecRows = 32;    // state rows per reduction tile
 constexpr int kDecMinRows = 8;  // fewest state rows per work-group when a head is split
+constexpr int kWideThreads = 1024;
+constexpr int kWideMaxElems = 10240;   // F (dv + 1) state floats of one head held in LDS (40 KB)
+constexpr int kWidePer = kWideMaxElems / kWideThreads;
 #ifndef LA_DECODE_TARGET_WGS
 #define LA_DECODE_TARGET_WGS 1024   // split heads until about this many work-groups launch
 #endif
@@ -133,6 +138,74 @@ __global__ __launch_bounds__(kDecThreads) void based_decode_kernel(const DecodeP
   }
 }
 
+// Heads whose whole state fits in LDS (F (dv + 1) <= kWideMaxElems): one work-group of
+// kWideThreads per head.  Every state element of the head is loaded at the start (one memory
+// latency instead of one per tile), updated in place, and its phi(q)-weighted value parked in
+// LDS; thread (segment, c) then adds rows [segment RS, (segment + 1) RS) of column c in row order
+// and thread c adds the segments in order (deterministic).
+__global__ __launch_bounds__(kWideThreads) void based_decode_wide_kernel(const DecodeParams p) {
+  __shared__ float xq[kDecMaxD], xk[kDecMaxD], vv[kDecMaxC];
+  __shared__ float phq[kDecMaxF], phk[kDecMaxF];
+  __shared__ float tile[kWideMaxElems];
+  __shared__ float part[kWideThreads];
+  __shared__ float den;
+  const int bh = blockIdx.x, tid = threadIdx.x;
+  const int d = p.d, dv = p.dv, F = p.F, C = dv + 1, FC = F * C;
+  float* __restrict__ st = p.state + (size_t)bh * FC;
+  float pre[kWidePer];
+#pragma unroll
+  for (int i = 0; i < kWidePer; ++i) {
+    const int e = tid + kWideThreads * i;
+    pre[i] = e < FC ? st[e] : 0.f;
+  }
+  if (tid < d) {
+    xq[tid] = load_elem(p.q, (size_t)bh * d + tid, p.in_f32);
+    xk[tid] = load_elem(p.k, (size_t)bh * d + tid, p.in_f32);
+  }
+  if (tid < dv) vv[tid] = load_elem(p.v, (size_t)bh * dv + tid, p.in_f32);
+  if (tid == 0) vv[dv] = 1.f;
+  __syncthreads();
+  const float rd = 1.0f / sqrtf((float)d), r4 = sqrtf(rd), rsq = rd * 0.70710678118654752f;
+  for (int f = tid; f < F; f += kWideThreads) {
+    phq[f] = feature(xq, f, d, r4, rsq, rd);
+    phk[f] = feature(xk, f, d, r4, rsq, rd);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kWidePer; ++i) {
+    const int e = tid + kWideThreads * i;
+    if (e < FC) {
+      const int fr = e / C, c = e - fr * C;
+      const float s = __builtin_fmaf(phk[fr], vv[c], pre[i]);
+      st[e] = s;
+      tile[e] = phq[fr] * s;
+    }
+  }
+  __syncthreads();
+  const int NS = kWideThreads / C, RS = (F + NS - 1) / NS;
+  const int seg = tid / C, col = tid - seg * C;
+  if (seg < NS) {
+    float r = 0.f;
+    const int r1 = min(F, (seg + 1) * RS);
+    for (int f = seg * RS; f < r1; ++f) r += tile[f * C + col];
+    part[seg * C + col] = r;
+  }
+  __syncthreads();
+  float colsum = 0.f;
+  if (tid < C)
+    for (int sg = 0; sg < NS; ++sg) colsum += part[sg * C + tid];
+  if (tid == dv) den = colsum;
+  __syncthreads();
+  if (tid < dv) {
+    const float y = p.normalize ? colsum / (den + p.eps) : colsum;
+    const size_t o = (size_t)bh * dv + tid;
+    if (p.out_f32)
+      static_cast<float*>(p.out)[o] = y;
+    else
+      static_cast<uint16_t*>(p.out)[o] = f32_to_bf16_bits(y);
+  }
+}
+
 // Head bh = blockIdx.x: column c = sum over groups g = 0 .. R-1 (in that order) of
 // part[(bh R + g) C + c], then the output as in the single-group kernel.
 __global__ __launch_bounds__(kDecThreads) void decode_combine_kernel(const DecodeParams p, int R,
@@ -179,7 +252,10 @@ static void decode_groups(long long BH, int d, int& R, int& RW) {
   R = (F + RW - 1) / RW;
 }
 
+static bool decode_wide(int d, int dv) { return (1 + d + d * (d + 1) / 2) * (dv + 1) <= kWideMaxElems; }
+
 size_t decode_workspace_bytes(long long BH, int d, int dv) {
+  if (decode_wide(d, dv)) return 0;
   int R, RW;
   decode_groups(BH, d, R, RW);
   return R > 1 ? (size_t)BH * R * (dv + 1) * sizeof(float) : 0;
@@ -200,6 +276,10 @@ int launch_decode_step(const DecodeArgs& a, hipStream_t stream) {
   p.normalize = a.normalize ? 1 : 0;
   p.in_f32 = a.in_f32 ? 1 : 0;
   p.out_f32 = a.out_f32 ? 1 : 0;
+  if (decode_wide(a.d, a.dv)) {
+    hipLaunchKernelGGL(based_decode_wide_kernel, dim3((unsigned)a.BH), dim3(kWideThreads), 0, stream, p);
+    return (int)hipGetLastError();
+  }
   int R = 1, RW = p.F;
   if (a.workspace != nullptr) decode_groups(a.BH, a.d, R, RW);
   if (R == 1) {
