@@ -1,4 +1,4 @@
-"""GPU parity of the decode step (la_based_decode_step): one token per head on the state the
+"""GPU parity of the decode step (la_based_decode_step{,_ws}): one token per head on the state the
 chunked kernel exports, against the fp64 oracle (dense BASED over the whole sequence, and the
 state's closed form sum_u phi(k_u) [v_u | 1])."""
 
