@@ -79,3 +79,26 @@ def test_decode_step_replays():
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, want) and torch.equal(st, st_eager)
+
+
+def test_sliding_identity_and_layer_replay():
+    """Sliding-window (resident and streaming windows), identity-map and full-layer calls captured
+    together in one graph; every replay matches the eager calls bit for bit."""
+    K = _kernels()
+    q, k, v = to_dev(*rand_qkv(2, 2, 700, 64, 64, seed=11, dtype=torch.bfloat16, scale_qk=0.5))
+    q16, k16 = to_dev(*rand_qkv(2, 2, 700, 16, 1, seed=12, dtype=torch.bfloat16, scale_qk=0.5))[:2]
+
+    def calls():
+        return (K.sliding_window_attn(q, k, v, window_size=64),
+                K.sliding_window_attn(q, k, v, window_size=300),
+                K.identity_linear_attn(q16, k16, v),
+                K.based_layer_attn(q16, k16, v, window_size=64, q_sw=q, k_sw=k))
+
+    want = calls()
+    g, outs = _capture(calls)
+    for _ in range(3):
+        _eager_noise(K)
+        g.replay()
+        torch.cuda.synchronize()
+        for y, w in zip(outs, want):
+            assert torch.equal(y, w)
