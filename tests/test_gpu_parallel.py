@@ -107,7 +107,7 @@ def test_config2_bf16(prescale):
     assert e < TOL_BF16
 
 
-def test_north_star_shape_prefix_and_spot_rows():
+def test_b2_h16_n8192_prefix_and_spot_rows():
     """B2 H16 N8192 d16 dv64 bf16: the first 2048 rows against the dense oracle (causal prefix
     invariance makes the prefix self-contained) and the last rows of two heads by a direct
     fp64 evaluation."""
