@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product package imports this module; only
 ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` use it,
-and only as the checker (or as the timed CPU baseline), never as the computation that is
+and only to check results (or as the timed CPU baseline), never as the computation that is
 shipped.
 
 It restates, line by line, the PyTorch math of the reference repository
