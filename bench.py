@@ -39,11 +39,11 @@ METRIC = "BASED fwd ms + TFLOP/s at B=2,H=16,N=8192,d=16,dv=64 (% MFMA/HBM roofl
 
 # (name, kind, B, H, N, d, dv, dtype, seed, chunk, window, prescale)
 CONFIGS = [
-    ("c1_parallel_fp32", "parallel", 1, 4, 1024, 16, 64, "f32", 0, 64, 64, True),
-    ("c2_parallel_bf16", "parallel", 2, 16, 2048, 16, 64, "bf16", 1, 64, 64, True),
-    ("c3_chunked_bf16", "chunked", 2, 16, 8192, 16, 64, "bf16", 2, 64, 64, True),
-    ("c4_sliding_bf16", "sliding", 2, 16, 4096, 64, 64, "bf16", 3, 64, 64, False),
-    ("c5_chunked_long_bf16", "chunked", 1, 16, 65536, 16, 64, "bf16", 4, 128, 64, True),
+    ("parallel_fp32_b1h4n1024", "parallel", 1, 4, 1024, 16, 64, "f32", 0, 64, 64, True),
+    ("parallel_bf16_b2h16n2048", "parallel", 2, 16, 2048, 16, 64, "bf16", 1, 64, 64, True),
+    ("chunked_bf16_b2h16n8192", "chunked", 2, 16, 8192, 16, 64, "bf16", 2, 64, 64, True),
+    ("sliding_w64_bf16_b2h16n4096", "sliding", 2, 16, 4096, 64, 64, "bf16", 3, 64, 64, False),
+    ("chunked_bf16_b1h16n65536", "chunked", 1, 16, 65536, 16, 64, "bf16", 4, 128, 64, True),
 ]
 HEADLINE = ("parallel_b2h16n8192", "parallel", 2, 16, 8192, 16, 64, "bf16", 2, 64, 64, True)
 

@@ -389,12 +389,12 @@ class Config:
 
 
 CONFIGS = {
-    "c1_parallel_fp32": Config("c1_parallel_fp32", "parallel", 1, 4, 1024, 16, 64, torch.float32, 0),
-    "c2_parallel_bf16": Config("c2_parallel_bf16", "parallel", 2, 16, 2048, 16, 64, torch.bfloat16, 1),
-    "c3_chunked_bf16": Config("c3_chunked_bf16", "chunked", 2, 16, 8192, 16, 64, torch.bfloat16, 2, chunk=64),
-    "c4_sliding_bf16": Config("c4_sliding_bf16", "sliding", 2, 16, 4096, 64, 64, torch.bfloat16, 3,
+    "parallel_fp32_b1h4n1024": Config("parallel_fp32_b1h4n1024", "parallel", 1, 4, 1024, 16, 64, torch.float32, 0),
+    "parallel_bf16_b2h16n2048": Config("parallel_bf16_b2h16n2048", "parallel", 2, 16, 2048, 16, 64, torch.bfloat16, 1),
+    "chunked_bf16_b2h16n8192": Config("chunked_bf16_b2h16n8192", "chunked", 2, 16, 8192, 16, 64, torch.bfloat16, 2, chunk=64),
+    "sliding_w64_bf16_b2h16n4096": Config("sliding_w64_bf16_b2h16n4096", "sliding", 2, 16, 4096, 64, 64, torch.bfloat16, 3,
                               window=64, prescale=False),
-    "c5_chunked_long_bf16": Config("c5_chunked_long_bf16", "chunked", 1, 16, 65536, 16, 64, torch.bfloat16, 4,
+    "chunked_bf16_b1h16n65536": Config("chunked_bf16_b1h16n65536", "chunked", 1, 16, 65536, 16, 64, torch.bfloat16, 4,
                                    chunk=128),
 }
 

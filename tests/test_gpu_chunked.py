@@ -111,9 +111,9 @@ def test_final_state_closed_form():
 
 
 @pytest.mark.parametrize("prescale", [True, False])
-def test_config3(prescale):
+def test_chunked_b2h16n8192(prescale):
     K = _kernels()
-    cfg = ref.CONFIGS["c3_chunked_bf16"]
+    cfg = ref.CONFIGS["chunked_bf16_b2h16n8192"]
     q, k, v = ref.config_inputs(cfg, prescale=prescale)
     y = K.based_chunked(*to_dev(q, k, v), chunk_size=cfg.chunk, out_dtype=torch.float32).cpu()
     n = 1024
@@ -121,13 +121,13 @@ def test_config3(prescale):
     e1 = err(y[:, :, :n], want)
     rows = torch.arange(cfg.N - 64, cfg.N)
     e2 = max(ref.rel_err(y[b, h, rows], _rows_fp64(q, k, v, b, h, rows)) for b, h in [(0, 0), (0, 7), (1, 15)])
-    print(f"config3 prescale={prescale} prefix err={e1:.3e} tail err={e2:.3e}")
+    print(f"chunked B2 H16 N8192 prescale={prescale} prefix err={e1:.3e} tail err={e2:.3e}")
     assert e1 < TOL and e2 < TOL
 
 
-def test_config5_long():
+def test_chunked_bf16_b1h16n65536():
     K = _kernels()
-    cfg = ref.CONFIGS["c5_chunked_long_bf16"]
+    cfg = ref.CONFIGS["chunked_bf16_b1h16n65536"]
     q, k, v = ref.config_inputs(cfg)
     y, st = K.based_chunked(*to_dev(q, k, v), chunk_size=cfg.chunk, out_dtype=torch.float32, return_state=True)
     y = y.cpu()
@@ -142,7 +142,7 @@ def test_config5_long():
     phik = ref.taylor_feature_map(k[0, 3].double())
     want_st = torch.cat([phik.T @ v[0, 3].double(), phik.sum(0).unsqueeze(-1)], dim=-1)
     e3 = ref.rel_err(st[0, 3].cpu(), want_st)
-    print(f"config5 prefix err={e1:.3e} rows err={e2:.3e} state err={e3:.3e}")
+    print(f"chunked B1 H16 N65536 prefix err={e1:.3e} rows err={e2:.3e} state err={e3:.3e}")
     assert e1 < TOL and e2 < TOL and e3 < 1e-2
 
 

@@ -83,27 +83,27 @@ def test_bf16_output_is_rounded_fp32_output():
     assert torch.equal(y16, y32.to(torch.bfloat16))
 
 
-def test_config1_fp32():
+def test_parallel_fp32_b1h4n1024():
     K = _kernels()
-    cfg = ref.CONFIGS["c1_parallel_fp32"]
+    cfg = ref.CONFIGS["parallel_fp32_b1h4n1024"]
     q, k, v = ref.config_inputs(cfg)
     y = K.solution_nki(*to_dev(q, k, v))
     assert y.dtype == torch.float32
     want, _, _ = ref.based_dense(q, k, v)
     e = err(y, want)
-    print(f"config1 fp32 err={e:.3e}")
+    print(f"parallel fp32 B1 H4 N1024 err={e:.3e}")
     assert e < TOL_F32
 
 
 @pytest.mark.parametrize("prescale", [True, False])
-def test_config2_bf16(prescale):
+def test_parallel_bf16_b2h16n2048(prescale):
     K = _kernels()
-    cfg = ref.CONFIGS["c2_parallel_bf16"]
+    cfg = ref.CONFIGS["parallel_bf16_b2h16n2048"]
     q, k, v = ref.config_inputs(cfg, prescale=prescale)
     y = K.based_parallel(*to_dev(q, k, v), out_dtype=torch.float32)
     want, _, _ = ref.based_dense(q, k, v)
     e = err(y, want)
-    print(f"config2 bf16 prescale={prescale} err={e:.3e}")
+    print(f"parallel bf16 B2 H16 N2048 prescale={prescale} err={e:.3e}")
     assert e < TOL_BF16
 
 

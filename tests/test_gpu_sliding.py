@@ -67,14 +67,14 @@ def test_full_window_is_causal_sdpa():
     assert err(y, want) < TOL_F32
 
 
-def test_config4_bf16():
+def test_sliding_w64_bf16_b2h16n4096():
     K = _kernels()
-    cfg = ref.CONFIGS["c4_sliding_bf16"]
+    cfg = ref.CONFIGS["sliding_w64_bf16_b2h16n4096"]
     q, k, v = ref.config_inputs(cfg)
     y = K.sliding_window_attn(*to_dev(q, k, v), window_size=cfg.window, out_dtype=torch.float32)
     want = ref.sliding_banded(q, k, v, window_size=cfg.window, dtype=torch.float64)
     e = err(y, want)
-    print(f"config4 err={e:.3e}")
+    print(f"sliding W64 B2 H16 N4096 err={e:.3e}")
     assert e < TOL_BF16
     y16 = K.nki_sliding_window_attn(*to_dev(q, k, v), window_size=cfg.window)
     assert y16.dtype == torch.bfloat16 and torch.equal(y16, y.to(torch.bfloat16))
