@@ -192,10 +192,19 @@ def time_calls(calls, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+def chunk_run(chunk):
+    """Tokens per chunk the chunked kernels run for a requested chunk size."""
+    c = int(_lib_handle().la_based_chunked_chunk_used(int(chunk)))
+    if c < 1:
+        raise RuntimeError(f"invalid chunk {chunk}")
+    return c
+
+
 def measure(cfg, steps, warmup, rotate, device, main_only=False):
     name, kind, B, H, N, d, dv, dt, seed, chunk, window, prescale = cfg
     esz = 2 if dt == "bf16" else 4
-    flop, nbytes = work(kind, B, H, N, d, dv, esz, chunk, window)
+    crun = chunk_run(chunk) if kind == "chunked" else chunk
+    flop, nbytes = work(kind, B, H, N, d, dv, esz, crun, window)
     hbm_bound = kind != "parallel"
     nsets = rotate if hbm_bound else 1
     calls = []
@@ -215,12 +224,13 @@ def measure(cfg, steps, warmup, rotate, device, main_only=False):
         "roofline_frac": round(max(t_mfma, t_hbm) / sec, 4),
         "flop": flop,
         "bytes": nbytes,
-        "shape": {"B": B, "H": H, "N": N, "d": d, "dv": dv, "dtype": dt, **({"chunk": chunk} if kind == "chunked" else {}),
+        "shape": {"B": B, "H": H, "N": N, "d": d, "dv": dv, "dtype": dt,
+                  **({"chunk": chunk, "chunk_run": crun} if kind == "chunked" else {}),
                   **({"window": window} if kind == "sliding" else {})},
         "input_sets": nsets,
     }
     if kind == "chunked":
-        res["tflops_f153"] = round(B * H * N * (4 * feature_dim(d) * dv + (chunk + 1) * (d + dv)) / sec / 1e12, 3)
+        res["tflops_f153"] = round(B * H * N * (4 * feature_dim(d) * dv + (crun + 1) * (d + dv)) / sec / 1e12, 3)
     del calls
     torch_empty_cache()
     return res
@@ -402,6 +412,53 @@ def cpu_baseline(chunk_heads, min_seconds=10.0):
     }
 
 
+def cpu_config_baseline(cfg, budget_s=3.0):
+    """CPU time of one configuration's call through the oracle's restatement of the reference's
+    PyTorch path, on this host's cores: per (b, h) head, as many heads as fit in ``budget_s``
+    (at least one), scaled to all B*H heads (heads are independent and equal in work).
+
+    * parallel: ``ref_based_attn`` (kernels/pytorch_attention.py:27-42) in the configuration's dtype;
+    * chunked: the dense phi-form ``ref_based_attn`` the reference's chunked benchmark times against
+      (benchmarks/chunked_attention_benchmark.py:55-65, fp32 inside) up to N = 8192; above that
+      (a t x t fp32 temporary of 17 GB per head) the oracle's chunk recurrence (fp32, the kernel's
+      chunk), which follows kernels/nki_attention_chunked.py:65-109;
+    * sliding: ``ref_sliding_window_attn`` (benchmarks/sliding_attention_benchmark.py:32-56)."""
+    import torch
+
+    from oracle import reference as ref
+
+    name, kind, B, H, N, d, dv, dt, seed, chunk, window, prescale = cfg
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(threads)
+    q, k, v = make_inputs(B, H, N, d, dv, dt, seed, prescale, "cpu")
+    q, k, v = (x.reshape(1, B * H, N, x.shape[-1]) for x in (q, k, v))
+    if kind == "parallel":
+        fn, what = ref.ref_based_attn, f"ref_based_attn (kernels/pytorch_attention.py:27-42) in {dt}"
+    elif kind == "chunked" and N <= 8192:
+        fn, what = ref.ref_based_attn_phi, "dense phi-form ref_based_attn (benchmarks/chunked_attention_benchmark.py:55-65)"
+    elif kind == "chunked":
+        crun = chunk_run(chunk)
+        fn = lambda a, b_, c: ref.based_chunked(a, b_, c, chunk=crun)
+        what = f"chunk recurrence (kernels/nki_attention_chunked.py:65-109), fp32, chunk {crun}"
+    else:
+        fn = lambda a, b_, c: ref.ref_sliding_window_attn(a, b_, c, window_size=window)
+        what = f"ref_sliding_window_attn (benchmarks/sliding_attention_benchmark.py:32-56), window {window}"
+    fn(q[:, :1], k[:, :1], v[:, :1])   # warm-up (allocator, thread pool)
+    heads = 0
+    t0 = time.perf_counter()
+    while True:
+        h = heads % (B * H)
+        fn(q[:, h:h + 1], k[:, h:h + 1], v[:, h:h + 1])
+        heads += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    sec = time.perf_counter() - t0
+    ms = sec / heads * B * H * 1e3
+    return {"ms": round(ms, 3), "cores": threads, "kind": "port",
+            "sample": f"{what}, {heads} head evaluations of {B * H} heads in {sec:.2f} s after one warm-up head, "
+                      f"scaled to all heads"}
+
+
 def load_traffic(kernel):
     path = os.path.join(ROOT, "profiles", f"traffic_{kernel}.json")
     if not os.path.exists(path):
@@ -466,6 +523,12 @@ def main():
             except RuntimeError as e:
                 per_config[cfg[0]] = {"error": str(e)}
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_chunk_heads)
+    if not args.no_cpu_baseline:
+        for cfg in CONFIGS:
+            res = per_config.get(cfg[0])
+            if res is not None and "ms" in res:
+                res["cpu_baseline"] = cpu_config_baseline(cfg)
+                res["cpu_baseline"]["gpu_speedup"] = round(res["cpu_baseline"]["ms"] / res["ms"], 1)
 
     achieved = head["tflops"]
     line = {

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 6
+#define LA_ABI_VERSION 7
 
 /* element types */
 #define LA_F32 0
@@ -101,9 +101,20 @@ int la_based_parallel_fwd_packed(const void* q, const void* k, const void* v, in
  * state_out_or_null: optional fp32 output of the final state per head, (B,H,F,dv+1) with the
  * K-sum in the last column.  workspace: device scratch of at least
  * la_based_chunked_workspace_bytes(...) bytes (may be NULL when that is 0).
- * Limits: d == 16, 1 <= dv <= 64, chunk in {16, 32, 64, 128, 256}.
+ * chunk: the reference's chunk_size, any value >= 1 (LA_ERR_BAD_SHAPE below 1).  The recurrence
+ * computes the same function for every chunk size (chunk-size invariance); it runs in chunks of
+ * la_based_chunked_chunk_used(chunk) tokens.
+ * Limits: d == 16, 1 <= dv <= 64.
  */
 size_t la_based_chunked_workspace_bytes(int B, int H, int N, int d, int dv, int chunk);
+
+/*
+ * Tokens per chunk the chunked kernels run for a requested chunk size (128 for every chunk >= 1;
+ * LA_ERR_BAD_SHAPE for chunk < 1).  The reference builds one NKI kernel per chunk_size
+ * (kernels/nki_attention_chunked.py:20-30); here the kernel's chunk is fixed and reported.
+ */
+int la_based_chunked_chunk_used(int chunk);
+
 int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dtype,
                          void* out, int out_dtype, int B, int H, int N, int d, int dv, int chunk,
                          float scale, float eps, int normalize,

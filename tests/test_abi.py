@@ -26,7 +26,8 @@ def _lib():
 def test_header_declares_expected_entry_points():
     assert _declared() == sorted([
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
-        "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_fwd", "la_based_chunked_fwd_continue", "la_sliding_window_fwd",
+        "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_chunk_used", "la_based_chunked_fwd",
+        "la_based_chunked_fwd_continue", "la_sliding_window_fwd",
         "la_sliding_window_fwd_add", "la_based_decode_step", "la_based_decode_workspace_bytes",
         "la_based_decode_step_ws", "la_identity_workspace_bytes", "la_identity_linear_fwd",
         "la_taylor_feature_map"])
@@ -40,7 +41,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib()
-    assert lib.la_abi_version() == 6
+    assert lib.la_abi_version() == 7
     for code in range(-9, 1):
         s = lib.la_status_string(code).decode()
         assert s and s != "unknown status"
@@ -262,6 +263,49 @@ def test_chunked_argument_errors():
     assert call(chunk=0) == -2
     assert call(scale=0.0) == -4
     assert call(N=0) == 0
+
+
+def test_chunked_chunk_argument():
+    """chunk is the reference's chunk_size: any value >= 1 is accepted (the recurrence gives the
+    same function for every chunk size) and the chunk the kernels run is reported."""
+    lib = _lib()
+    assert lib.la_based_chunked_chunk_used(0) == -2
+    assert lib.la_based_chunked_chunk_used(-5) == -2
+    for c in (1, 16, 64, 100, 128, 256, 4096):
+        assert lib.la_based_chunked_chunk_used(c) == 128
+    # the workspace does not depend on the requested chunk
+    sizes = {lib.la_based_chunked_workspace_bytes(2, 16, 8192, 16, 64, c) for c in (1, 64, 128, 1000)}
+    assert len(sizes) == 1
+    f = lib.la_based_chunked_fwd
+    assert f(P, P, P, 1, P, 1, 2, 16, 8192, 16, 64, 0, 0.25, 1e-6, 0, P, 1 << 30, None, None) == -2
+
+
+def test_lds_copy_carries_its_wait_states():
+    """The global -> LDS copies are inline assembly, in front of which the compiler inserts no
+    wait states: the copy itself must hold the five that a VALU write of its descriptor SGPRs
+    needs, and it must be the only LDS-DMA instruction written by hand."""
+    import glob
+    csrc = os.path.join(ROOT, "trainium-linear-attention_amd", "csrc")
+    hits = []
+    for path in sorted(glob.glob(os.path.join(csrc, "*.hip")) + glob.glob(os.path.join(csrc, "*.hpp"))):
+        text = open(path).read()
+        for m in re.finditer(r"asm volatile\((.*?)\);", text, re.S):
+            if "lds\"" in m.group(1) or "offen lds" in m.group(1):
+                hits.append((os.path.basename(path), m.group(1)))
+    assert len(hits) == 1 and hits[0][0] == "la_common.hpp", hits
+    nops = re.findall(r"s_nop (\d+)", hits[0][1])
+    assert nops and int(nops[0]) >= 4
+    assert hits[0][1].index("s_nop") < hits[0][1].index("buffer_load")
+
+
+def test_reference_import_line():
+    """The reference's callers import the dense function and the NKI wrapper by these names
+    (benchmarks/based_attention_benchmark.py:19)."""
+    from kernels.pytorch_attention import ref_based_attn, solution_nki  # noqa: F401
+    import torch
+    q = torch.zeros(1, 1, 4, 16)
+    with pytest.raises(RuntimeError):
+        ref_based_attn(q, q, q)
 
 
 def test_feature_map_argument_errors():

@@ -937,12 +937,22 @@ void segment_split(int BH, int N, int& P, int& seg_chunks) {
 
 }  // namespace
 
+int chunked_chunk_tokens() { return CH; }
+
 size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk) {
   if (d != 16 || dv > 64 || chunk < 1) return (size_t)-1;
   int P, seg_chunks;
   segment_split(BH, N, P, seg_chunks);
   const size_t per = (size_t)64 * NF * 2 + (size_t)1024 * 4;
   return (size_t)BH * P * per + 256;
+}
+
+size_t chunked_scratch_bytes(int BH, int N, int d, int dv, bool with_state) {
+  if (d != 16 || dv > 64) return (size_t)-1;
+  int P, seg_chunks;
+  segment_split(BH, N, P, seg_chunks);
+  if (P == 1 && !with_state) return 0;
+  return chunked_workspace_bytes(BH, N, d, dv, 1);
 }
 
 int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {

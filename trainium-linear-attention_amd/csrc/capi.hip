@@ -131,6 +131,11 @@ size_t la_based_chunked_workspace_bytes(int B, int H, int N, int d, int dv, int 
   return la::chunked_workspace_bytes(B * H, N, d, dv, chunk);
 }
 
+int la_based_chunked_chunk_used(int chunk) {
+  if (chunk < 1) return LA_ERR_BAD_SHAPE;
+  return la::chunked_chunk_tokens();
+}
+
 static int chunked_common(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
                           int H, int N, int d, int dv, int chunk, float scale, float eps, int normalize,
                           void* workspace, size_t workspace_bytes, const float* state_in, long long prev_tokens,
@@ -140,7 +145,7 @@ static int chunked_common(const void* q, const void* k, const void* v, int in_dt
   if (!finite_f(scale) || !(scale > 0.f) || !finite_f(eps) || eps < 0.f) return LA_ERR_BAD_SCALAR;
   if (chunk < 1) return LA_ERR_BAD_SHAPE;
   if ((long long)B * H * N == 0) return LA_OK;
-  const size_t need = la::chunked_workspace_bytes(B * H, N, d, dv, chunk);
+  const size_t need = la::chunked_scratch_bytes(B * H, N, d, dv, state_in != nullptr);
   if (need == (size_t)-1) return LA_ERR_UNSUPPORTED_DIM;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
   if (state_out_or_null != nullptr && (reinterpret_cast<uintptr_t>(state_out_or_null) & 3)) return LA_ERR_BAD_ALIGNMENT;

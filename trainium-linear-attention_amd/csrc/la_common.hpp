@@ -138,9 +138,14 @@ __device__ __forceinline__ u32x4 buffer_rsrc(const void* base, u32 bytes) {
 // (lds_base wave-uniform).  Issued as inline assembly so that the compiler's wait-count pass does
 // not treat every later LDS read as dependent on the copy: the caller orders copies and reads
 // itself, with s_waitcnt vmcnt and a barrier.  Each call adds one to the wave's vmcnt.
+//
+// The compiler inserts no wait states in front of inline assembly, so the copy carries its
+// own: a VALU write of an SGPR (v_readfirstlane of the descriptor in buffer_rsrc) needs five
+// wait states before a VMEM instruction reads that SGPR, and an SALU write of M0 one before an
+// LDS-DMA copy.  s_nop 4 provides five, whatever the scheduler placed just before the copy.
 __device__ __forceinline__ void lds_copy16(const u32x4& rsrc, u32 lds_base, int voff) {
   asm volatile(
-      "s_nop 0\n\t"   // M0 written by SALU just before an LDS copy needs one wait state
+      "s_nop 4\n\t"
       "buffer_load_dwordx4 %0, %1, 0 offen lds"
       :
       : "v"(voff), "s"(rsrc), "{m0}"(lds_base)

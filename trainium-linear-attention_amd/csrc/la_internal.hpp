@@ -87,6 +87,10 @@ int launch_based_parallel(const ParallelArgs& a, hipStream_t stream);
 size_t parallel_workspace_bytes(int BH, int N, int d, int dv, bool in_f32);
 int launch_sliding_window(const SlidingArgs& a, hipStream_t stream);
 size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk);
+int chunked_chunk_tokens();   // tokens per chunk of the chunked kernels
+// Bytes of scratch the chunked kernels actually use for this call: 0 when the sequence is one
+// segment and there is no initial state, (size_t)-1 for unsupported shapes.
+size_t chunked_scratch_bytes(int BH, int N, int d, int dv, bool with_state);
 int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream);
 int launch_feature_map(const FeatureMapArgs& a, hipStream_t stream);
 int device_cu_count();   // compute units of the current device (256 when the query fails)

@@ -15,9 +15,10 @@ kernels/nki_attention_chunked.py:92-102).  dv may differ from d.
 
 The chunked kernel covers bf16 inputs with d = 16 and dv <= 64 (the BASED configuration).
 Other shapes and fp32 inputs are computed by the fused parallel kernel, which evaluates the
-same function (numerator or normalised) on the GPU.  ``chunk_size`` is accepted for signature
-compatibility; the kernel's recurrence uses 64-token chunks, which gives the same result for
-every chunk size up to rounding (chunk-size invariance of the recurrence).
+same function (numerator or normalised) on the GPU.  ``chunk_size`` is the reference's argument
+(any value >= 1); the kernel's recurrence runs 128-token chunks (``la_based_chunked_chunk_used``
+reports it), which gives the same result for every chunk size up to rounding (chunk-size
+invariance of the recurrence).
 """
 
 from __future__ import annotations

@@ -15,8 +15,12 @@ Behavioural differences, all deliberate:
   (the reference's ``solution`` swallows kernel exceptions, :87-92);
 * dv may differ from d (the reference wrapper reshapes v to d, :60);
 * no padding copies: ragged t, any d <= 128 and dv <= 128 are handled in-kernel.
-The reference's dense PyTorch ``ref_based_attn`` is a test oracle, not a kernel path; it
-lives with the other oracles outside this package.
+
+``ref_based_attn(q, k, v, eps=1e-6)`` keeps the reference's name (:27-42) so that its callers'
+``from kernels.pytorch_attention import ref_based_attn, solution_nki`` resolves; on GPU
+tensors it runs the fused kernel, i.e. it is the same computation as ``solution_nki`` and not
+an independent check.  The reference's dense PyTorch restatement used as the test oracle lives
+outside this package.
 """
 
 from __future__ import annotations
@@ -27,7 +31,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["solution_nki", "solution", "based_parallel"]
+__all__ = ["solution_nki", "solution", "based_parallel", "ref_based_attn"]
 
 
 def _compute_dtype(dt: torch.dtype) -> torch.dtype:
@@ -96,6 +100,17 @@ def solution_nki(q, k, v, eps=1e-6):
     """BASED causal attention via the fused MI355X kernel (reference :44-78).
 
     q, k: (b, h, t, d); v: (b, h, t, dv).  Returns (b, h, t, dv) in q.dtype.
+    """
+    return based_parallel(q, k, v, eps=eps)
+
+
+def ref_based_attn(q, k, v, eps=1e-6):
+    """The reference's ``ref_based_attn`` entry point (:27-42), run by the fused kernel.
+
+    Same signature and function (s = (q/sqrt(d)).k, p = 1 + s + s^2/2, causal,
+    y = (p @ v) / (sum p + eps), output in q.dtype); computed on the GPU by
+    ``la_based_parallel_fwd`` with fp32 accumulation instead of the reference's
+    input-dtype arithmetic.  Tensors must be on a ROCm device.
     """
     return based_parallel(q, k, v, eps=eps)
 
