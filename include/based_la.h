@@ -39,6 +39,10 @@ extern "C" {
 #define LA_ERR_NO_DEVICE (-7)
 #define LA_ERR_BAD_ALIGNMENT (-8)
 #define LA_ERR_OVERLAP (-9)
+#define LA_ERR_SCRATCH_LIMIT (-10)
+
+/* Size of the device array behind la_based_chunked_fwd_noalloc, per device. */
+#define LA_NOALLOC_SCRATCH_BYTES (32u << 20)
 
 /* Version of this ABI (LA_ABI_VERSION). */
 int la_abi_version(void);
@@ -135,6 +139,21 @@ int la_based_chunked_fwd_continue(const void* q, const void* k, const void* v, i
                                   int chunk, float scale, float eps, int normalize,
                                   void* workspace, size_t workspace_bytes, const float* state_in,
                                   long long prev_tokens, float* state_out_or_null, void* hip_stream);
+
+/*
+ * la_based_chunked_fwd without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ * No counterpart in the reference.  The kernels' scratch is a fixed device array of
+ * LA_NOALLOC_SCRATCH_BYTES inside the library (one per device, held until the process ends);
+ * shapes that would need more return LA_ERR_SCRATCH_LIMIT (32 MiB covers every shape: at most
+ * about 1022 (head, segment) records of 24 KiB are used).  The call allocates nothing.  Calls
+ * that overlap in time on one device share the array and race: serialise them (one stream, or
+ * the caller's own ordering).  Other arguments, limits and results as la_based_chunked_fwd.
+ */
+int la_based_chunked_fwd_noalloc(const void* q, const void* k, const void* v, int in_dtype,
+                                 void* out, int out_dtype, int B, int H, int N, int d, int dv,
+                                 int chunk, float scale, float eps, int normalize,
+                                 float* state_out_or_null, void* hip_stream);
 
 /*
  * Causal sliding-window softmax attention.

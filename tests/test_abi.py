@@ -27,7 +27,7 @@ def test_header_declares_expected_entry_points():
     assert _declared() == sorted([
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
         "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_chunk_used", "la_based_chunked_fwd",
-        "la_based_chunked_fwd_continue", "la_sliding_window_fwd",
+        "la_based_chunked_fwd_continue", "la_based_chunked_fwd_noalloc", "la_sliding_window_fwd",
         "la_sliding_window_fwd_add", "la_based_decode_step", "la_based_decode_workspace_bytes",
         "la_based_decode_step_ws", "la_identity_workspace_bytes", "la_identity_linear_fwd",
         "la_taylor_feature_map"])
@@ -42,7 +42,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_status_strings():
     lib = _lib()
     assert lib.la_abi_version() == 7
-    for code in range(-9, 1):
+    for code in range(-10, 1):
         s = lib.la_status_string(code).decode()
         assert s and s != "unknown status"
 
@@ -278,6 +278,25 @@ def test_chunked_chunk_argument():
     assert len(sizes) == 1
     f = lib.la_based_chunked_fwd
     assert f(P, P, P, 1, P, 1, 2, 16, 8192, 16, 64, 0, 0.25, 1e-6, 0, P, 1 << 30, None, None) == -2
+
+
+def test_chunked_noalloc_argument_errors():
+    """The no-allocation chunked entry point validates like la_based_chunked_fwd and rejects
+    shapes whose scratch exceeds its fixed device array before touching the device."""
+    lib = _lib()
+    f = lib.la_based_chunked_fwd_noalloc
+
+    def call(q=P, chunk=64, d=16, dv=64, B=2, H=16, N=8, scale=0.25, eps=1e-6, dt=1):
+        return f(q, P, P, dt, P, 1, B, H, N, d, dv, chunk, scale, eps, 1, None, None)
+
+    assert call(q=None) == -1
+    assert call(chunk=0) == -2
+    assert call(d=32) == -5
+    assert call(dv=65) == -5
+    assert call(N=0) == 0
+    assert call(dt=5) == -3
+    # largest scratch need below the limit: 511 heads x 2 segments of 24 KiB records
+    assert lib.la_based_chunked_workspace_bytes(1, 511, 256, 16, 64, 64) <= (32 << 20)
 
 
 def test_lds_copy_carries_its_wait_states():

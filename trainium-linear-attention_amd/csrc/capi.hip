@@ -5,6 +5,8 @@
 // and nothing is allocated.
 #include <math.h>
 
+#include <mutex>
+
 #include "../../include/based_la.h"
 #include "la_internal.hpp"
 
@@ -48,6 +50,7 @@ const char* la_status_string(int status) {
     case LA_ERR_NO_DEVICE: return "no HIP device";
     case LA_ERR_BAD_ALIGNMENT: return "tensor pointer not aligned to its element size";
     case LA_ERR_OVERLAP: return "input and output buffers overlap";
+    case LA_ERR_SCRATCH_LIMIT: return "shape needs more scratch than the no-allocation entry point's fixed device array";
     default: break;
   }
   if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
@@ -186,6 +189,74 @@ int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dty
                          void* workspace, size_t workspace_bytes, float* state_out_or_null, void* hip_stream) {
   return chunked_common(q, k, v, in_dtype, out, out_dtype, B, H, N, d, dv, chunk, scale, eps, normalize, workspace,
                         workspace_bytes, nullptr, 0, state_out_or_null, hip_stream);
+}
+
+}  // extern "C"
+
+// ---- no-allocation variant of la_based_chunked_fwd
+//
+// The chunked kernels' scratch (per (head, segment) state increments and their prefixes) lives
+// in a file-scope device array instead of a caller workspace.  Host code never passes the
+// array's name to a kernel: its device address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and kept in g_scratch_ptr.  Every call on a
+// device shares that device's array; the kernels write every scratch word they read before
+// reading it, so nothing needs clearing between calls, but calls that overlap on one device
+// (different streams, or host threads) race on it.
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[LA_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the device that owns `stream` (the current device for the null
+// stream), looked up on the first call for that device.
+int scratch_for_stream(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (stream != nullptr) {
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) return LA_ERR_NO_DEVICE;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return LA_ERR_NO_DEVICE;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return LA_ERR_NO_DEVICE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return LA_ERR_NO_DEVICE;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return LA_ERR_NO_DEVICE;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return LA_ERR_NO_DEVICE;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int la_based_chunked_fwd_noalloc(const void* q, const void* k, const void* v, int in_dtype, void* out,
+                                 int out_dtype, int B, int H, int N, int d, int dv, int chunk, float scale,
+                                 float eps, int normalize, float* state_out_or_null, void* hip_stream) {
+  int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
+  if (rc != LA_OK) return rc;
+  if (chunk < 1) return LA_ERR_BAD_SHAPE;
+  if ((long long)B * H * N == 0) return LA_OK;
+  const size_t need = la::chunked_scratch_bytes(B * H, N, d, dv, false);
+  if (need == (size_t)-1) return LA_ERR_UNSUPPORTED_DIM;
+  if (need > (size_t)LA_NOALLOC_SCRATCH_BYTES) return LA_ERR_SCRATCH_LIMIT;
+  void* ws = nullptr;
+  if (need > 0) {
+    rc = scratch_for_stream(static_cast<hipStream_t>(hip_stream), &ws);
+    if (rc != LA_OK) return rc;
+  }
+  return chunked_common(q, k, v, in_dtype, out, out_dtype, B, H, N, d, dv, chunk, scale, eps, normalize, ws,
+                        need > 0 ? (size_t)LA_NOALLOC_SCRATCH_BYTES : 0, nullptr, 0, state_out_or_null, hip_stream);
 }
 
 int la_based_chunked_fwd_continue(const void* q, const void* k, const void* v, int in_dtype, void* out,

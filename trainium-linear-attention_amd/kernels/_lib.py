@@ -44,6 +44,9 @@ _SIGNATURES = {
     "la_based_chunked_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
                                       _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int, _c_void,
                                       _c_size, _c_void, _c_void]),
+    "la_based_chunked_fwd_noalloc": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
+                                              _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int, _c_void,
+                                              _c_void]),
     "la_sliding_window_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
                                        _c_int, _c_int, _c_int, _c_int, _c_float, _c_void]),
     "la_sliding_window_fwd_add": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int,
