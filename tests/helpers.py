@@ -38,3 +38,22 @@ def rounded_err(y, want):
     y = y.detach().cpu().double()
     want = want.double()
     return ((y - want).abs() / (want.abs() + want.pow(2).mean().sqrt())).max().item()
+
+
+def rows_fp64(q, k, v, b, h, rows, eps=1e-6, normalize=True):
+    """Dense fp64 BASED output of the given query rows of head (b, h) over all earlier keys:
+    the oracle for a few rows of a sequence too long for the dense t x t form."""
+    import math
+    qq, kk, vv = q[b, h].double(), k[b, h].double(), v[b, h].double()
+    d = qq.shape[-1]
+    s = (qq[rows] / math.sqrt(d)) @ kk.T
+    mask = torch.arange(qq.shape[0]).unsqueeze(0) <= rows.unsqueeze(1)
+    p = (1 + s + 0.5 * s * s) * mask
+    num = p @ vv
+    return num / (p.sum(-1, keepdim=True) + eps) if normalize else num
+
+
+def head_errs(y, want):
+    """Parity metric per (b, h) head: each head normalised by its own rms."""
+    y = y.detach().cpu()
+    return [ref.rel_err(y[b, h], want[b, h]) for b in range(y.shape[0]) for h in range(y.shape[1])]

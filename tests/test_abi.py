@@ -83,6 +83,11 @@ def test_parallel_argument_errors():
     assert call(ws=ctypes.c_void_p(24)) == -8
     assert call(N=0) == 0          # empty: nothing to launch
     assert call(B=0) == 0
+    need32 = lib.la_based_parallel_workspace_bytes(1, 1, 8, 32, 64, 1)
+    assert call(d=32, ws=None, ws_bytes=0) == -6      # bf16 register-staged shapes need the |v| maxima
+    assert call(d=32, ws_bytes=need32 - 4) == -6
+    assert call(dt=0, odt=0, ws=None, ws_bytes=0, q=ctypes.c_void_p(1 << 20), k=ctypes.c_void_p(1 << 21),
+                v=ctypes.c_void_p(1 << 22), out=ctypes.c_void_p(1 << 23), N=0) == 0   # fp32: no workspace
 
 
 def test_sliding_add_argument_errors():
@@ -230,9 +235,10 @@ def test_parallel_workspace_sizes():
     assert ws(2, 16, 8192, 16, 64, 1) == 32 * 128 * (9216 + 4 * (64 + 160))
     assert ws(1, 1, 65, 16, 32, 1) == 2 * (5120 + 4 * (32 + 160))
     assert ws(1, 1, 64, 16, 64, 0) == 0        # fp32 inputs: no workspace
-    assert ws(1, 1, 64, 32, 64, 1) == 0        # d != 16
-    assert ws(1, 1, 64, 16, 60, 1) == 0        # dv % 8 != 0
-    assert ws(1, 1, 64, 16, 72, 1) == 0        # dv > 64
+    # other bf16 shapes (register-staged kernel): 64 partial maxima of |v| per head
+    assert ws(1, 1, 64, 32, 64, 1) == 256       # d != 16
+    assert ws(1, 1, 64, 16, 60, 1) == 256       # dv % 8 != 0
+    assert ws(2, 3, 64, 16, 72, 1) == 6 * 256   # dv > 64
     assert ws(0, 1, 64, 16, 64, 1) == 0
 
 

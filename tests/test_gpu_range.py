@@ -1,0 +1,170 @@
+"""Numeric range of the bf16 kernels: inputs far from N(0, 1) against the fp64 oracle.
+
+The bf16 kernels run their products on fp16 MFMAs (V, the rounded polynomial, the features and
+the chunked state), whose range is 2^-14 .. 65504 against bf16's 2^-126 .. 3.4e38.  These cases
+hold each kernel to the bf16 bar (max|y - y_ref| / rms(y_ref) < 2e-2 per head, fp32 output) for
+bf16 inputs of any magnitude the reference's own bf16 arithmetic handles
+(kernels/pytorch_attention.py:35-41): V scaled by 1e5 and 1e-6, heads of different scales in one
+call, blocks of one head on both sides of the kernels' scale steps, scores s = q.k/sqrt(d) up to
+about 300, a mean-biased V over 65536 tokens (its sums grow linearly with N), the long-context
+configuration without pre-scaling, and a continuation from a state with a large sum of v.
+"""
+
+import pytest
+import torch
+
+from oracle import reference as ref
+from tests.helpers import err, head_errs, rand_qkv, rows_fp64, to_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _kernels():
+    import kernels
+    return kernels
+
+
+def _scaled(B, H, N, d, dv, seed, vscale=1.0, qk=0.5, vbias=0.0):
+    q, k, v = rand_qkv(B, H, N, d, dv, seed=seed, dtype=torch.float32, scale_qk=qk)
+    v = v * torch.as_tensor(vscale, dtype=torch.float32) + vbias
+    return q.bfloat16(), k.bfloat16(), v.bfloat16()
+
+
+def _run(path, q, k, v, normalize=True):
+    K = _kernels()
+    qd, kd, vd = to_dev(q, k, v)
+    if path == "parallel":
+        return K.based_parallel(qd, kd, vd, normalize=normalize, out_dtype=torch.float32)
+    return K.based_chunked(qd, kd, vd, normalize=normalize, out_dtype=torch.float32)
+
+
+# (d, dv): the packed parallel kernel (d 16, dv % 8 == 0, dv <= 64), the register-staged one
+# (d 32; dv 96) and the chunked kernel's shapes
+PAR_SHAPES = [(16, 64), (16, 40), (32, 64), (16, 96)]
+
+
+@pytest.mark.parametrize("vscale", [1e5, 1e-6, 3e4, 2e-5])
+@pytest.mark.parametrize("d,dv", PAR_SHAPES)
+def test_parallel_v_scale(vscale, d, dv):
+    q, k, v = _scaled(1, 2, 1100, d, dv, seed=11, vscale=vscale)
+    want, want_num, _ = ref.based_dense(q, k, v)
+    e = max(head_errs(_run("parallel", q, k, v), want))
+    en = max(head_errs(_run("parallel", q, k, v, normalize=False), want_num))
+    print(f"parallel d={d} dv={dv} v x {vscale:g}: err={e:.3e} num_err={en:.3e}")
+    assert e < TOL and en < TOL
+
+
+@pytest.mark.parametrize("vscale", [1e5, 1e-6, 3e4])
+@pytest.mark.parametrize("dv", [64, 24])
+def test_chunked_v_scale(vscale, dv):
+    q, k, v = _scaled(1, 2, 3000, 16, dv, seed=12, vscale=vscale)
+    want, want_num, _ = ref.based_dense(q, k, v)
+    e = max(head_errs(_run("chunked", q, k, v), want))
+    en = max(head_errs(_run("chunked", q, k, v, normalize=False), want_num))
+    print(f"chunked dv={dv} v x {vscale:g}: err={e:.3e} num_err={en:.3e}")
+    assert e < TOL and en < TOL
+
+
+@pytest.mark.parametrize("path,d,dv", [("parallel", 16, 64), ("parallel", 32, 64), ("chunked", 16, 64)])
+def test_heads_of_different_scales(path, d, dv):
+    """One call, four heads at V scales 1e5, 1, 1e-6 and 1e-3: each head on its own scale."""
+    q, k, v = _scaled(1, 4, 1500, d, dv, seed=13, vscale=torch.tensor([1e5, 1.0, 1e-6, 1e-3]).view(1, 4, 1, 1))
+    want, _, _ = ref.based_dense(q, k, v)
+    errs = head_errs(_run(path, q, k, v), want)
+    print(f"{path} d={d} dv={dv} per-head errs " + " ".join(f"{x:.2e}" for x in errs))
+    assert max(errs) < TOL
+
+
+@pytest.mark.parametrize("path,d,dv", [("parallel", 16, 64), ("parallel", 16, 96), ("chunked", 16, 64)])
+def test_scale_steps_within_a_head(path, d, dv):
+    """V magnitudes that put the 64-key blocks (and 128-token chunks) of one head on different
+    sides of the kernels' power-of-two scale steps: |v| near 128, and a head whose first 300
+    tokens are 1e6 times smaller than the rest."""
+    q, k, v = _scaled(1, 2, 2600, d, dv, seed=14, vscale=40.0)
+    t = torch.ones(1, 2, 2600, 1)
+    t[:, 1, :300] = 1e-6
+    v2 = (v.float() * t).bfloat16()
+    for vv in (v, v2):
+        want, _, _ = ref.based_dense(q, k, vv)
+        errs = head_errs(_run(path, q, k, vv), want)
+        print(f"{path} d={d} dv={dv} errs " + " ".join(f"{x:.2e}" for x in errs))
+        assert max(errs) < TOL
+
+
+@pytest.mark.parametrize("path,d,dv", [("parallel", 16, 64), ("parallel", 32, 64), ("parallel", 16, 96),
+                                       ("chunked", 16, 64)])
+def test_large_scores(path, d, dv):
+    """q, k ~ N(0, 7.5^2): typical |s| = |q.k|/sqrt(d) around 60 and the largest near 300, where
+    p = 1 + s + s^2/2 reaches 4.5e4."""
+    q, k, v = _scaled(1, 2, 1200, d, dv, seed=15, qk=7.5)
+    s = (q[0, 0].double() @ k[0, 0].double().T) / d ** 0.5
+    smax = s.tril().abs().max().item()
+    want, _, _ = ref.based_dense(q, k, v)
+    e = max(head_errs(_run(path, q, k, v), want))
+    print(f"{path} d={d} dv={dv} max|s|={smax:.0f} err={e:.3e}")
+    assert smax > 250
+    assert e < TOL
+
+
+def _long_checks(y, q, k, v, heads, st=None, n=1024):
+    """Prefix rows against the dense oracle (causal prefix invariance), spot rows against fp64
+    over all earlier keys, the exported state against its closed form."""
+    y = y.cpu()
+    want, _, _ = ref.based_dense(q[:, heads, :n], k[:, heads, :n], v[:, heads, :n])
+    e1 = max(head_errs(y[:, heads, :n], want))
+    e2 = 0.0
+    N = q.shape[2]
+    for h in heads:
+        for r0 in (N // 3, N - 32):
+            rows = torch.arange(r0, r0 + 32)
+            e2 = max(e2, ref.rel_err(y[0, h, rows], rows_fp64(q, k, v, 0, h, rows)))
+    e3 = 0.0
+    if st is not None:
+        h = heads[0]
+        phik = ref.taylor_feature_map(k[0, h].double())
+        want_st = torch.cat([phik.T @ v[0, h].double(), phik.sum(0).unsqueeze(-1)], dim=-1)
+        e3 = ref.rel_err(st[0, h].cpu(), want_st)
+    return e1, e2, e3
+
+
+def test_biased_v_b1h4n65536():
+    """v = randn + 1 over 65536 tokens: sum v and every sum phi_f(k) v grow linearly with N."""
+    K = _kernels()
+    q, k, v = _scaled(1, 4, 65536, 16, 64, seed=16, qk=1.0, vbias=1.0)
+    y, st = K.based_chunked(*to_dev(q, k, v), out_dtype=torch.float32, return_state=True)
+    e1, e2, e3 = _long_checks(y, q, k, v, [0, 3], st)
+    print(f"biased v N65536: prefix err={e1:.3e} rows err={e2:.3e} state err={e3:.3e}")
+    assert e1 < TOL and e2 < TOL and e3 < 1e-2
+
+
+def test_chunked_b1h16n65536_unscaled():
+    """The long-context configuration without dividing q and k by sqrt(d)."""
+    K = _kernels()
+    cfg = ref.CONFIGS["chunked_bf16_b1h16n65536"]
+    q, k, v = ref.config_inputs(cfg, prescale=False)
+    y, st = K.based_chunked(*to_dev(q, k, v), chunk_size=cfg.chunk, out_dtype=torch.float32, return_state=True)
+    e1, e2, e3 = _long_checks(y, q, k, v, [0, 9], st)
+    print(f"B1 H16 N65536 unscaled: prefix err={e1:.3e} rows err={e2:.3e} state err={e3:.3e}")
+    assert e1 < TOL and e2 < TOL and e3 < 1e-2
+
+
+def test_continue_from_large_state():
+    """A 60000-token prefill of v = randn + 2 exported as a state (sum v ~ 1.2e5 per column),
+    then 2000 more tokens continued from it: rows against fp64 over the whole sequence."""
+    K = _kernels()
+    q, k, v = _scaled(1, 2, 62000, 16, 64, seed=17, qk=1.0, vbias=2.0)
+    qd, kd, vd = to_dev(q, k, v)
+    n0 = 60000
+    _, st = K.based_chunked(qd[:, :, :n0], kd[:, :, :n0], vd[:, :, :n0], out_dtype=torch.float32, return_state=True)
+    assert st[0, 0, 0, :64].abs().max().item() > 1e5
+    y2 = K.based_chunked(qd[:, :, n0:], kd[:, :, n0:], vd[:, :, n0:], out_dtype=torch.float32, state_in=st,
+                         prev_tokens=n0).cpu()
+    e = 0.0
+    for h in (0, 1):
+        for r0 in (0, 1000, 1968):
+            rows = torch.arange(n0 + r0, n0 + r0 + 32)
+            e = max(e, ref.rel_err(y2[0, h, r0:r0 + 32], rows_fp64(q, k, v, 0, h, rows)))
+    print(f"continuation from a large state: rows err={e:.3e}")
+    assert e < TOL

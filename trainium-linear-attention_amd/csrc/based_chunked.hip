@@ -10,15 +10,27 @@
 //   * Every product runs on v_mfma_f32_32x32x16_f16 (the 16x16x32 forms issue at half the
 //     rate on gfx950).  Chunks are 128 tokens; wave w of a work-group owns query tokens
 //     32w .. 32w+31 of every chunk.
-//   * phi is never materialised in HBM.  With q~ = alpha q and k~ = beta k (alpha beta = scale)
-//     the kernel works in units of 2p:  2 p(s) = 2 + 2 s + s^2 = sum_f qf(q~) kf(k~), over 160
-//     feature slots (10 K-steps of 16) holding the 153 distinct features of the symmetric
-//     Taylor map: the constant, q~_i, q~_i^2 and q~_i q~_j (i < j).  The q side of a K-step is
-//     four packed-fp16 products of q~'s eight register pairs R_x = (q~_2x, q~_2x+1); the two
-//     lane halves of the MFMA operand hold q~ rotated by two registers, so one v_pk_mul_f16
-//     yields two features for each half ("templates" below).  The k side multiplies two rows of
-//     an LDS table [k~ | 1 | 0 | 2] (K^T, token pairs packed), again one v_pk_mul_f16 per two
-//     products; the factor 2 of the linear and mixed terms is on the q side.
+//   * phi is never materialised in HBM.  With q~ = k~-scale = sqrt(scale) (q, k) the kernel works
+//     in units of p/2:  2 p(s) = 2 + 2 s + s^2 = sum_f qf(q~) kf(k~), over 160 feature slots
+//     (10 K-steps of 16) holding the 153 distinct features of the symmetric Taylor map: the
+//     constant, q~_i, q~_i^2 and q~_i q~_j (i < j); the k side carries a factor 1/4, so the
+//     products sum to p/2.  The q side of a K-step is four packed-fp16 products of q~'s eight
+//     register pairs R_x = (q~_2x, q~_2x+1); the two lane halves of the MFMA operand hold q~
+//     rotated by two registers, so one v_pk_mul_f16 yields two features for each half
+//     ("templates" below).  The k side multiplies two rows of an LDS table
+//     [k~/2 | 1/2 | 0 | 1] (K^T, token pairs packed), again one v_pk_mul_f16 per two products
+//     (each product is 1/4 of k~_i k~_j, k~_i, 2); the factor 2 of the linear and mixed terms is
+//     on the q side.
+//   * Range.  fp16 (2^-14 .. 65504) carries the features, V, the state and the Gram matrix, so
+//     every fp16 copy of a growing or data-sized quantity has a power-of-two exponent: V and the
+//     state in registers share one exponent U per work-group (V is converted as fp16(v 2^-U) and
+//     the state accumulates in units of 2^U); at every chunk boundary the waves exchange
+//     max |S| and the next chunk's max |v| through LDS at the barrier they already pass, and U
+//     rises (the state registers rescaled) when either would leave fp16 -- a rare event, since
+//     U steps up by several binades at once.  The Gram matrix published for the denominator has
+//     its own exponent; the state increments and prefixes in the workspace carry one exponent
+//     per (head, segment).  Intra-chunk scores are b/2 = 1/2 + q~.k~/2 (an MFMA started from the
+//     inline constant 0.5), so P/4 = (b/2)^2 + 1/4 stays in fp16 for |s| up to about 510.
 //   * The state S (160 x dv, fp32 MFMA accumulators) stays in registers across chunks,
 //     partitioned over the waves by blocks of 32 features; every chunk it is published to LDS
 //     as fp16 S^T for the inter-chunk product phi(Q) S of all waves.
@@ -48,7 +60,8 @@ constexpr int QRS = 24;         // row stride (halves) of the q~ / k~ row tables
 constexpr int KRS = 136;        // row stride (halves) of the K^T and V^T tables: 272 B
 constexpr int STS = 168;        // row stride (halves) of S^T: 336 B
 constexpr int KT_ROWS = 20;
-constexpr int R_ONES = 16, R_ZA = 17, R_ZB = 18, R_TWOS = 19;   // constant rows of K^T
+constexpr int R_ONES = 16, R_ZA = 17, R_ZB = 18, R_TWOS = 19;   // constant rows of K^T: 1/2, 0, 0, 1
+constexpr int kNoExp = -128;    // exponent of an all-zero quantity (below every other)
 constexpr int NWAVE_OUT = 4;
 constexpr int NWAVE_SEG = 5;
 constexpr int MAX_SEG = 32;
@@ -99,8 +112,8 @@ __host__ __device__ constexpr KRows krows(int f) {
 }
 
 // Reference feature (benchmarks/chunked_attention_benchmark.py:34-53 order: 1, x_i, x_i^2,
-// x_i x_j for i < j row-major) of slot f, and the factor from the internal k side to it as
-// an index into {1/2, 2^(sigma/2), 2^sigma/sqrt 2, 2^sigma}; ref = -1 for unused slots.
+// x_i x_j for i < j row-major) of slot f, and the factor from the k side of 2p (four times the
+// table products) to it as an index into {1/2, 1, 1/sqrt 2, 1}; ref = -1 for unused slots.
 struct RefFeat {
   int ref, fac;
 };
@@ -136,12 +149,14 @@ struct ChunkParams {
   const uint16_t* v;
   void* out;
   float* state_out;
-  uint16_t* wsS;    // [BH][P][64][NF] fp16 S^T increments, then prefixes
+  uint16_t* wsS;    // [BH][P][64][NF] fp16 S^T increments, then prefixes, in units of 2^wsE / 2^wsEP
   float* wsG;       // [BH][P][64 lanes][16] fp32 Gram increments (accumulator layout), then prefixes
+  int* wsE;         // [BH][P] exponent of each increment (slot P - 1: the imported state)
+  int* wsEP;        // [BH][P] exponent of each prefix
   int BH, N, dv, P, seg_chunks;
-  float alpha, beta;                 // q~ = alpha q, k~ = beta k
+  float qs, ks;                      // q~ = qs q (= sqrt(scale) q); K^T table rows ks k = q~-scale k / 2
   float eps;
-  float st_fac[4];                   // internal -> reference feature factors (state export)
+  float st_fac[4];                   // k side of 2p -> reference feature factors (state export)
   float st_inv[4];                   // their inverses (initial state import)
   const float* state_in;             // optional initial state, reference basis (BH, 153, dv + 1)
   float prev_tokens;                 // tokens summarised by state_in (0 without one)
@@ -169,7 +184,11 @@ struct OutLds {
   uint16_t KT[KT_ROWS * KRS];   // k~^T, constant rows
   uint16_t VT[64 * KRS];        // V^T, 16-byte units swizzled by row (vt_off)
   uint16_t ST[64 * STS];        // S^T (feature slots)
-  uint16_t G16[32 * GRS];       // Gram matrix [k~ | 1]^T [k~ | 1] of earlier tokens, (16,16) zeroed
+  uint16_t G16[32 * GRS];       // Gram matrix of [k~/2 | 1/2] over earlier tokens in units of 2^eg, (16,16) zeroed
+  u32 xs[2][NWAVE_OUT];         // per wave, by chunk parity: max |S| (fp32 bits) before the update
+  u32 xv[2][NWAVE_OUT];         // max |v| (bf16 bits) of the next chunk
+  u32 xk[2][NWAVE_OUT];         // max |k| (bf16 bits) of the next chunk
+  int eg;                       // exponent of G16
 };
 struct SegTables {
   uint16_t KT[KT_ROWS * KRS];
@@ -197,7 +216,7 @@ __device__ __forceinline__ int vt_off(int c, int u) { return c * KRS + 8 * (u ^ 
 __device__ __forceinline__ void init_kt_constants(uint16_t* KT, int tid, int nthreads) {
   for (int i = tid; i < 4 * (CH / 2); i += nthreads) {
     const int row = R_ONES + (i >> 6), col = 2 * (i & 63);
-    const u32 val = row == R_ONES ? 0x3c003c00u : (row == R_TWOS ? 0x40004000u : 0u);
+    const u32 val = row == R_ONES ? 0x38003800u : (row == R_TWOS ? 0x3c003c00u : 0u);
     *reinterpret_cast<u32*>(&KT[row * KRS + col]) = val;
   }
 }
@@ -271,8 +290,9 @@ __device__ __forceinline__ u32 swap_quad_pairs(u32 x) {
   return (u32)__builtin_amdgcn_mov_dpp((int)x, 0x4e, 0xf, 0xf, false);
 }
 
+// q~, k~/2 pieces (stage_convert_qk) and V^T pairs as fp16(v vs) (stage_convert_v).
 template <bool WITH_Q>
-__device__ __forceinline__ void stage_convert(const StageRegs& s, StageConv& o, float alpha, float beta, int l) {
+__device__ __forceinline__ void stage_convert_qk(const StageRegs& s, StageConv& o, float alpha, float beta, int l) {
   if (WITH_Q) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -294,6 +314,13 @@ __device__ __forceinline__ void stage_convert(const StageRegs& s, StageConv& o, 
     for (int i = 0; i < 4; ++i)
       o.kr[i] = pack_f16x2(beta * bf16_lo_to_f32(s.k[i]), beta * bf16_hi_to_f32(s.k[i]));
   }
+}
+
+// The kernels' main path converts V as is (exponent 0, the usual case); when a work-group's
+// exponent is not 0 a separate rare path converts it again with stage_convert_v_scaled and
+// rewrites the table before the readers' barrier.  (One conversion with a run-time choice
+// between the two costs registers the segment kernel does not have at three waves per SIMD.)
+__device__ __forceinline__ void stage_convert_v(const StageRegs& s, StageConv& o) {
 #pragma unroll
   for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
@@ -303,6 +330,108 @@ __device__ __forceinline__ void stage_convert(const StageRegs& s, StageConv& o, 
       o.vt[pp][2 * w + 1] = pack_f16x2(bf16_hi_to_f32(a), bf16_hi_to_f32(b));
     }
   }
+}
+
+__device__ __forceinline__ void stage_convert_v_scaled(const StageRegs& s, StageConv& o, float vs) {
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const u32 a = s.v[pp][0][w], b = s.v[pp][1][w];
+      o.vt[pp][2 * w] = pack_f16x2(bf16_lo_to_f32(a) * vs, bf16_lo_to_f32(b) * vs);
+      o.vt[pp][2 * w + 1] = pack_f16x2(bf16_hi_to_f32(a) * vs, bf16_hi_to_f32(b) * vs);
+    }
+  }
+}
+
+// Wave-wide maxima of two 16-bit values at once, packed (hi, lo) into one word: the DPP steps of
+// wave_max_u32 on v_pk_max_u16.
+__device__ __forceinline__ u32 wave_max_u16x2(u32 x) {
+  typedef __attribute__((__vector_size__(2 * sizeof(unsigned short)))) unsigned short u16x2;
+  auto step = [](u32 a, u32 b) -> u32 {
+    return __builtin_bit_cast(u32, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+  };
+  x = step(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false));
+  x = step(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false));
+  x = step(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false));
+  x = step(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false));
+  x = step(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
+  x = step(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
+  return (u32)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// Largest |k| of this thread's staged k values, as bf16 magnitude bits.
+__device__ __forceinline__ u32 stage_kmax(const StageRegs& s) {
+  typedef __attribute__((__vector_size__(2 * sizeof(unsigned short)))) unsigned short u16x2;
+  u16x2 m = {0, 0};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, s.k[w] & 0x7fff7fffu));
+  return max((u32)m[0], (u32)m[1]);
+}
+
+// Largest |v| of this thread's staged V values, as bf16 magnitude bits.
+__device__ __forceinline__ u32 stage_vmax(const StageRegs& s) {
+  typedef __attribute__((__vector_size__(2 * sizeof(unsigned short)))) unsigned short u16x2;
+  u16x2 m = {0, 0};
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2, s.v[pp][j][w] & 0x7fff7fffu));
+  return max((u32)m[0], (u32)m[1]);
+}
+
+// Largest |x| over an accumulator array, as fp32 bits.
+template <int NB>
+__device__ __forceinline__ u32 acc_absmax(const f32x16 (&S)[NB][2]) {
+  float m = 0.f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) m = __builtin_fmaxf(m, __builtin_fabsf(S[b][n][i]));
+  return __builtin_bit_cast(u32, m);
+}
+
+// floor(log2 x) of a positive fp32 magnitude given by its bits; kNoExp for zero.
+__device__ __forceinline__ int exp_of_f32bits(u32 b) { return b == 0u ? kNoExp : (int)(b >> 23) - 127; }
+
+// The largest of four per-wave maxima in LDS, as a wave-uniform (scalar) value: every lane
+// reads the same words, and readfirstlane tells the compiler so, which keeps the decisions
+// taken on it uniform branches.
+__device__ __forceinline__ u32 lds_max4(const u32* x) {
+  return (u32)__builtin_amdgcn_readfirstlane((int)max(max(x[0], x[1]), max(x[2], x[3])));
+}
+
+// Exponent of the first chunk from floor(log2 max |v|): 0 while max |v| lies in [2^-6, 2^13)
+// (V^T is then v itself in fp16, without a multiply), else the one that puts max |v| in
+// [2^7, 2^8); an all-zero chunk leaves a placeholder that the first nonzero V raises.
+__device__ __forceinline__ int first_unit(int eV) {
+  if (eV == kNoExp) return -200;
+  return (eV >= -6 && eV <= 12) ? 0 : eV - 7;
+}
+
+// State / V exponent after a chunk: U rises (never falls) when the state registers reach 2^14
+// (new U puts them below 2^10) or the next chunk's V would reach 2^15 in units of 2^U (new U
+// puts it below 2^8).  eS, eV: floor(log2) of max |S| (units of 2^U) and max |v|.
+__device__ __forceinline__ int next_unit(int U, int eS, int eV) {
+  int n = U;
+  if (eS >= 14) n = max(n, U + eS - 9);
+  if (eV - n >= 15) n = max(n, eV - 7);
+  return n;
+}
+
+template <int NB>
+__device__ __forceinline__ void acc_scale(f32x16 (&S)[NB][2], float f) {
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) S[b][n][i] *= f;
 }
 
 // Keeps the conversion above this point (the compiler would otherwise sink it next to the LDS
@@ -320,6 +449,18 @@ __device__ __forceinline__ void stage_pin(StageConv& o) {
     for (int i = 0; i < 8; i += 4) asm volatile("" : "+v"(o.vt[pp][i]), "+v"(o.vt[pp][i + 1]), "+v"(o.vt[pp][i + 2]), "+v"(o.vt[pp][i + 3]));
 }
 
+__device__ __forceinline__ void stage_write_v(const StageConv& o, uint16_t* VT, int l, int wv) {
+#pragma unroll
+  for (int pp = 0; pp < 2; ++pp) {
+    const int tp = 16 * wv + 8 * pp + (l >> 3);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = 8 * (l & 7) + e;
+      *reinterpret_cast<u32*>(&VT[vt_off(d, tp >> 2) + 2 * (tp & 3)]) = o.vt[pp][e];
+    }
+  }
+}
+
 template <bool WITH_Q>
 __device__ __forceinline__ void stage_write(const StageConv& o, uint16_t* Q0, uint16_t* Kr, uint16_t* KT, uint16_t* VT,
                                             int l, int wv) {
@@ -335,15 +476,7 @@ __device__ __forceinline__ void stage_write(const StageConv& o, uint16_t* Q0, ui
 #pragma unroll
     for (int i = 0; i < 4; ++i) *reinterpret_cast<u32*>(&KT[(d0 + i) * KRS + 2 * tp]) = o.kt[i];
   }
-#pragma unroll
-  for (int pp = 0; pp < 2; ++pp) {
-    const int tp = 16 * wv + 8 * pp + (l >> 3);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = 8 * (l & 7) + e;
-      *reinterpret_cast<u32*>(&VT[vt_off(d, tp >> 2) + 2 * (tp & 3)]) = o.vt[pp][e];
-    }
-  }
+  stage_write_v(o, VT, l, wv);
 }
 
 // ---- state update of NB blocks of 32 feature slots over one chunk (all dv)
@@ -400,6 +533,8 @@ constexpr int SEG_PER_WG = 2;
 template <bool VEC_V>
 __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_kernel(const ChunkParams p) {
   __shared__ __attribute__((aligned(16))) SegLds Ls[SEG_PER_WG];
+  __shared__ u32 vx[2][SEG_PER_WG][4];      // max |v| of the next chunk per staging wave (by chunk parity)
+  __shared__ u32 smx[SEG_PER_WG][NWAVE_SEG];   // max |S| per wave at the end
   const int wall = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int sub = wall / NWAVE_SEG, w = wall - sub * NWAVE_SEG;
   const int tid = threadIdx.x - sub * 64 * NWAVE_SEG, lane = tid & 63;
@@ -429,13 +564,35 @@ __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_k
   StageRegs sa, sb;
   StageConv cv;
   const int last = c0 + nch - 1;
+  // V exponent of this half (Uo) and of the other one (Ux): every wave tracks both, so that the
+  // rare extra barrier below is taken by the whole work-group; S accumulates in units of 2^Uo
+  static_assert(SEG_PER_WG == 2, "two halves");
+  int Uo, Ux;
+  auto publish_vmax = [&](int par, const StageRegs& x, bool has) {
+    const u32 m = wave_max_u32(has ? stage_vmax(x) : 0u);
+    if (w < 4 && lane == 0) vx[par][sub][w] = m;
+  };
+  auto read_vexp = [&](int par, int sb_) -> int { return exp_of_f32bits(lds_max4(vx[par][sb_]) << 16); };
   if (stager) {
     stage_load<VEC_V, false>(sa, p, nullptr, kh, vh, c0 * CH, lane, w);
     stage_load<VEC_V, false>(sb, p, nullptr, kh, vh, min(c0 + 1, last) * CH, lane, w, nch > 1);
-    stage_convert<false>(sa, cv, p.alpha, p.beta, lane);
+  }
+  publish_vmax(0, sa, stager);
+  if (stager) {
+    stage_convert_qk<false>(sa, cv, p.qs, p.ks, lane);
+    stage_convert_v(sa, cv);
     stage_write<false>(cv, nullptr, nullptr, L.buf[0].KT, L.buf[0].VT, lane, w);
   }
   lds_barrier();
+  Uo = first_unit(read_vexp(0, sub));
+  Ux = first_unit(read_vexp(0, sub ^ 1));
+  if (Uo != 0 || Ux != 0) {   // V outside [2^-6, 2^13): convert the first chunk again, scaled
+    if (Uo != 0 && stager) {
+      stage_convert_v_scaled(sa, cv, __builtin_ldexpf(1.0f, -Uo));
+      stage_write_v(cv, L.buf[0].VT, lane, w);
+    }
+    lds_barrier();
+  }
   auto step = [&](int c, StageRegs& nxt, StageRegs& ahead) {
     // nxt holds chunk c + 1; ahead (free) receives chunk c + 2.  Issued by every wave (empty for
     // the non-staging one) so that the wait for nxt below counts only older loads.
@@ -443,36 +600,69 @@ __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_k
     const SegTables& T = L.buf[c & 1];
     update_blocks<1>(T.KT, T.VT, S, ra, rb, r, h);
     gram_update(T.KT, G, grow, h, w, NWAVE_SEG);
-    if (stager && c + 1 < nch) {
-      SegTables& U = L.buf[(c + 1) & 1];
-      stage_convert<false>(nxt, cv, p.alpha, p.beta, lane);
+    const bool more = stager && c + 1 < nch;
+    publish_vmax((c + 1) & 1, nxt, more);
+    if (more) {
+      SegTables& Tn = L.buf[(c + 1) & 1];
+      stage_convert_qk<false>(nxt, cv, p.qs, p.ks, lane);
+      stage_convert_v(nxt, cv);
       stage_pin<false>(cv);
-      stage_write<false>(cv, nullptr, nullptr, U.KT, U.VT, lane, w);
+      stage_write<false>(cv, nullptr, nullptr, Tn.KT, Tn.VT, lane, w);
     }
     lds_barrier();
+    // a half whose next V needs a higher exponent raises it and rescales its state; a half at
+    // exponent != 0 converts that V again, scaled, reloading it rather than keeping its
+    // registers across the barrier (uniform over the work-group)
+    const int Uon = next_unit(Uo, kNoExp, read_vexp((c + 1) & 1, sub));
+    const int Uxn = next_unit(Ux, kNoExp, read_vexp((c + 1) & 1, sub ^ 1));
+    if (c + 1 < nch && (Uon != Uo || Uxn != Ux || Uon != 0 || Uxn != 0)) {
+      if (Uon != Uo) acc_scale<1>(S, __builtin_ldexpf(1.0f, Uo - Uon));
+      if (Uon != 0 && more) {
+        StageRegs again;
+        stage_load<VEC_V, false>(again, p, nullptr, kh, vh, (c0 + c + 1) * CH, lane, w);
+        stage_convert_v_scaled(again, cv, __builtin_ldexpf(1.0f, -Uon));
+        stage_write_v(cv, L.buf[(c + 1) & 1].VT, lane, w);
+      }
+      Uo = Uon;
+      Ux = Uxn;
+      lds_barrier();
+    }
   };
   for (int c = 0; c < nch; c += 2) {
     step(c, sb, sa);
     if (c + 1 < nch) step(c + 1, sa, sb);
   }
-  // increment: S^T fp16 [dv][slot]; Gram partials of the waves summed through LDS
+  // increment: S^T fp16 [dv][slot] in units of 2^EI, EI from max |S| over the waves (values
+  // below 2^14); Gram partials of the waves summed through LDS
   const size_t slot = (size_t)bh * p.P + seg;
   uint16_t* ws = p.wsS + slot * (64 * NF);
-#pragma unroll
-  for (int n = 0; n < (active ? 2 : 0); ++n) {
-#pragma unroll
-    for (int J = 0; J < 2; ++J) {
-      const f32x16& a = S[0][n];
-      const u32x4 pk = {pack_f16x2(a[8 * J + 0], a[8 * J + 1]), pack_f16x2(a[8 * J + 2], a[8 * J + 3]),
-                        pack_f16x2(a[8 * J + 4], a[8 * J + 5]), pack_f16x2(a[8 * J + 6], a[8 * J + 7])};
-      *reinterpret_cast<u32x4*>(&ws[(32 * n + r) * NF + 32 * w + 16 * J + 8 * h]) = pk;
-    }
+  {
+    const u32 m = wave_max_u32(acc_absmax<1>(S));
+    if (lane == 0) smx[sub][w] = m;
   }
   float* red = reinterpret_cast<float*>(&L);   // 5 x 64 x 16 floats = 20 KB, tables no longer read
 #pragma unroll
   for (int e = 0; e < 16; e += 4)
     *reinterpret_cast<f32x4*>(&red[(w * 64 + lane) * 16 + e]) = (f32x4){G[e], G[e + 1], G[e + 2], G[e + 3]};
   lds_barrier();
+  u32 msub = 0u;
+#pragma unroll
+  for (int i = 0; i < NWAVE_SEG; ++i) msub = max(msub, smx[sub][i]);
+  msub = (u32)__builtin_amdgcn_readfirstlane((int)msub);
+  const int eS = exp_of_f32bits(msub);
+  const int EI = eS == kNoExp ? kNoExp : Uo + eS - 13;
+  const float f = eS == kNoExp ? 0.f : __builtin_ldexpf(1.0f, 13 - eS);
+#pragma unroll
+  for (int n = 0; n < (active ? 2 : 0); ++n) {
+#pragma unroll
+    for (int J = 0; J < 2; ++J) {
+      const f32x16& a = S[0][n];
+      const u32x4 pk = {pack_f16x2(a[8 * J + 0] * f, a[8 * J + 1] * f), pack_f16x2(a[8 * J + 2] * f, a[8 * J + 3] * f),
+                        pack_f16x2(a[8 * J + 4] * f, a[8 * J + 5] * f), pack_f16x2(a[8 * J + 6] * f, a[8 * J + 7] * f)};
+      *reinterpret_cast<u32x4*>(&ws[(32 * n + r) * NF + 32 * w + 16 * J + 8 * h]) = pk;
+    }
+  }
+  if (w == 0 && lane == 0 && active) p.wsE[slot] = EI;
   if (w == 0 && active) {
     float* gout = p.wsG + slot * 1024 + lane * 16;
 #pragma unroll
@@ -488,24 +678,35 @@ __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_k
 // -------------------------------------------------------------------------------------------
 // Initial state (continuation): the caller's [S | z] in the reference feature basis
 // (benchmarks/chunked_attention_benchmark.py:34-53 order), converted to the internal basis in
-// slot P - 1 of every head: S^T slot f = S_ref[ref(f)] / factor (fp16 [64][NF]); the Gram matrix
-// of [k~ | 1] in the accumulator layout [64 lanes][16], entry (i, j) = the k-sum of the feature
-// it carries / factor: (16, 16) the count, (i, 16) linear, (i, i) square, (i, j) pair -- the
-// inverse of the state export at the end of output_wave.
+// slot P - 1 of every head: S^T slot f = S_ref[ref(f)] / (4 factor) (fp16 [64][NF] in units of
+// 2^wsE, wsE from the largest entry); the Gram matrix of [k~/2 | 1/2] in the accumulator layout
+// [64 lanes][16], entry (i, j) = the k-sum of the feature it carries / (4 factor): (16, 16) the
+// count, (i, 16) linear, (i, i) square, (i, j) pair -- the inverse of the state export at the
+// end of output_wave.
 __global__ __launch_bounds__(256) void chunked_import_kernel(const ChunkParams p) {
+  __shared__ u32 wm[4];
   const int bh = blockIdx.x, tid = threadIdx.x, dv = p.dv;
   const float* si = p.state_in + (size_t)bh * 153 * (dv + 1);
   const size_t slot = (size_t)bh * p.P + (p.P - 1);
   uint16_t* ws = p.wsS + slot * (64 * NF);
-  for (int idx = tid; idx < 64 * NF; idx += 256) {
+  auto value = [&](int idx) -> float {
     const int c = idx / NF, f = idx - c * NF;
     float x = 0.f;
     if (c < dv && f < 160) {
       const RefFeat rf = ref_feature(f);
-      if (rf.ref >= 0) x = si[(size_t)rf.ref * (dv + 1) + c] * p.st_inv[rf.fac];
+      if (rf.ref >= 0) x = si[(size_t)rf.ref * (dv + 1) + c] * (0.25f * p.st_inv[rf.fac]);
     }
-    ws[idx] = (uint16_t)(pack_f16x2(x, 0.f) & 0xffffu);
-  }
+    return x;
+  };
+  float m = 0.f;
+  for (int idx = tid; idx < 64 * NF; idx += 256) m = __builtin_fmaxf(m, __builtin_fabsf(value(idx)));
+  const u32 mw = wave_max_u32(__builtin_bit_cast(u32, m));
+  if ((tid & 63) == 0) wm[tid >> 6] = mw;
+  __syncthreads();
+  const int eS = exp_of_f32bits(max(max(wm[0], wm[1]), max(wm[2], wm[3])));
+  const float f = eS == kNoExp ? 0.f : __builtin_ldexpf(1.0f, 13 - eS);
+  if (tid == 0) p.wsE[slot] = eS == kNoExp ? kNoExp : eS - 13;
+  for (int idx = tid; idx < 64 * NF; idx += 256) ws[idx] = (uint16_t)(pack_f16x2(value(idx) * f, 0.f) & 0xffffu);
   float* g = p.wsG + slot * 1024;
   for (int idx = tid; idx < 1024; idx += 256) {
     const int lane = idx >> 4, e = idx & 15, r = lane & 31, h = lane >> 5;
@@ -523,7 +724,7 @@ __global__ __launch_bounds__(256) void chunked_import_kernel(const ChunkParams p
         x = si[(size_t)(33 + lo * (31 - lo) / 2 + (hi - lo - 1)) * (dv + 1) + dv] * p.st_inv[3];   // pair
       }
     }
-    g[idx] = x;
+    g[idx] = 0.25f * x;
   }
 }
 
@@ -532,6 +733,10 @@ __global__ __launch_bounds__(256) void chunked_import_kernel(const ChunkParams p
 // the increments of segments 0 .. p-1.  Thread (head, 8-byte unit), fp32 accumulation, the loads
 // of up to 16 segments in flight at once.
 // With an initial state the scan starts from slot P - 1 (written by chunked_import_kernel).
+// Exponents: increment s is fp16 in units of 2^wsE[s] (entries below 2^14); the prefix through
+// s, a sum of n such increments, is stored in units of 2^wsEP[s] with wsEP[s] = max wsE +
+// ceil(log2 n), which keeps it below 2^14 whatever the signs (the same for every thread, so
+// thread 0 of the head's first work-group writes it).
 __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p) {
   constexpr int US = 64 * NF / 4, UG = 1024 / 2;   // 8-byte units of S^T (fp16) and G (fp32)
   const int e = blockIdx.x * 256 + threadIdx.x, bh = blockIdx.y;
@@ -539,15 +744,27 @@ __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p
   const bool init = p.state_in != nullptr;
   if (e < US) {
     uint16_t* base = p.wsS + (size_t)bh * p.P * (64 * NF) + 4 * (size_t)e;
+    // the head's exponents, read once into scalar registers (uniform addresses); fully unrolled
+    // over MAX_SEG so that every index is a constant
+    const int* exg = p.wsE + (size_t)bh * p.P;
+    int ex[MAX_SEG];
+#pragma unroll
+    for (int i = 0; i < MAX_SEG; ++i) ex[i] = i < p.P ? __builtin_amdgcn_readfirstlane(exg[i]) : kNoExp;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    int emax = kNoExp, cnt = 0;
     if (init) {
       const u32x2 x0 = *reinterpret_cast<const u32x2*>(base + (size_t)nseg * (64 * NF));
-      acc[0] = f16_lo_to_f32(x0[0]);
-      acc[1] = f16_hi_to_f32(x0[0]);
-      acc[2] = f16_lo_to_f32(x0[1]);
-      acc[3] = f16_hi_to_f32(x0[1]);
+      emax = exg[nseg];
+      cnt = 1;
+      const float f0 = emax == kNoExp ? 0.f : __builtin_ldexpf(1.0f, emax);
+      acc[0] = f16_lo_to_f32(x0[0]) * f0;
+      acc[1] = f16_hi_to_f32(x0[0]) * f0;
+      acc[2] = f16_lo_to_f32(x0[1]) * f0;
+      acc[3] = f16_hi_to_f32(x0[1]) * f0;
     }
-    for (int s0 = 0; s0 < nseg; s0 += 16) {
+#pragma unroll
+    for (int s0 = 0; s0 < MAX_SEG; s0 += 16) {
+      if (s0 >= nseg) break;
       u32x2 x[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i)
@@ -555,12 +772,19 @@ __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         if (s0 + i >= nseg) break;
-        acc[0] += f16_lo_to_f32(x[i][0]);
-        acc[1] += f16_hi_to_f32(x[i][0]);
-        acc[2] += f16_lo_to_f32(x[i][1]);
-        acc[3] += f16_hi_to_f32(x[i][1]);
+        const int es = ex[s0 + i];
+        const float fs = es == kNoExp ? 0.f : __builtin_ldexpf(1.0f, es);
+        emax = max(emax, es);
+        ++cnt;
+        const int ep = emax == kNoExp ? kNoExp : emax + (cnt > 1 ? 32 - __builtin_clz((unsigned)(cnt - 1)) : 0);
+        const float fo = ep == kNoExp ? 0.f : __builtin_ldexpf(1.0f, -ep);
+        acc[0] += f16_lo_to_f32(x[i][0]) * fs;
+        acc[1] += f16_hi_to_f32(x[i][0]) * fs;
+        acc[2] += f16_lo_to_f32(x[i][1]) * fs;
+        acc[3] += f16_hi_to_f32(x[i][1]) * fs;
         *reinterpret_cast<u32x2*>(base + (size_t)(s0 + i) * (64 * NF)) =
-            (u32x2){pack_f16x2(acc[0], acc[1]), pack_f16x2(acc[2], acc[3])};
+            (u32x2){pack_f16x2(acc[0] * fo, acc[1] * fo), pack_f16x2(acc[2] * fo, acc[3] * fo)};
+        if (e == 0) p.wsEP[(size_t)bh * p.P + s0 + i] = ep;
       }
     }
   } else if (e < US + UG) {
@@ -610,18 +834,33 @@ __device__ __forceinline__ void publish_state(OutLds& L, const f32x16 (&S)[NB][2
 }
 
 // fp16 Gram matrix for the denominator, with the token count G(16,16) left out (it is added
-// exactly).  Lane (col j = r, rows 8 jj + 4 h + i) writes row j by symmetry.
+// exactly), in units of 2^eg with eg from its largest entry (entries below 2^14).  Lane (col
+// j = r, rows 8 jj + 4 h + i) writes row j by symmetry.
 __device__ __forceinline__ void publish_gram(OutLds& L, const f32x16& G, int r, int h) {
+  float g[16];
+  float m = 0.f;
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj) {
-    float g0 = G[4 * jj], g1 = G[4 * jj + 1], g2 = G[4 * jj + 2], g3 = G[4 * jj + 3];
-    if (jj == 2 && h == 0 && r == 16) g0 = 0.f;
-    *reinterpret_cast<u32x2*>(&L.G16[r * GRS + 8 * jj + 4 * h]) = (u32x2){pack_f16x2(g0, g1), pack_f16x2(g2, g3)};
+  for (int e = 0; e < 16; ++e) {
+    g[e] = (e == 8 && h == 0 && r == 16) ? 0.f : G[e];
+    m = __builtin_fmaxf(m, __builtin_fabsf(g[e]));
   }
+  const int eg0 = exp_of_f32bits(wave_max_u32(__builtin_bit_cast(u32, m)));
+  const int eg = eg0 == kNoExp ? 0 : eg0 - 13;
+  const float f = __builtin_ldexpf(1.0f, -eg);
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj)
+    *reinterpret_cast<u32x2*>(&L.G16[r * GRS + 8 * jj + 4 * h]) =
+        (u32x2){pack_f16x2(g[4 * jj] * f, g[4 * jj + 1] * f), pack_f16x2(g[4 * jj + 2] * f, g[4 * jj + 3] * f)};
+  if (r == 0 && h == 0) L.eg = eg;
 }
 
 // VEC: v rows 16-byte aligned with dv % 8 == 0 and out 16-byte aligned with dv % 4 == 0 (buffer
 // loads and stores); otherwise element-wise accesses with bounds checks.
+//
+// Units: the state registers S hold (sum phi_k v) / 4 in units of 2^U (the k-side table carries
+// the 1/4), the published S^T is fp16(S), V^T is fp16(v 2^-U), the intra-chunk P is fp16(p / 2),
+// so O = S^T phi(Q)^T + V^T P^T is num / 2 in units of 2^U.  The Gram registers G hold
+// (sum g g^T) / 4 and the published copy G16 is fp16(G 2^-EG).
 template <int W, bool VEC, bool OUT_F32>
 __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int bh, int seg) {
   using OB = OwnedBlocks<W>;
@@ -665,6 +904,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
     S[b][1] = splat16(0.f);
   }
   f32x16 G = splat16(0.f);
+  int U = kNoExp;   // exponent of the state registers and of V^T (the same in every wave)
   StageRegs st;
   StageConv cv;
   stage_load<VEC, true>(st, p, qh, kh, vh, c0 * CH, lane, W);
@@ -672,6 +912,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
     // prefix of the earlier segments (with the caller's initial state, when there is one); the
     // first segment's is slot P - 1, which holds the initial state alone
     const size_t slot = (size_t)bh * p.P + (seg > 0 ? seg - 1 : p.P - 1);
+    U = seg > 0 ? p.wsEP[slot] : p.wsE[slot];
     const uint16_t* ws = p.wsS + slot * (64 * NF);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -702,16 +943,50 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
     }
   }
 
+  // Exponent of the first chunk: at least the prefix's, else first_unit of the chunk's max |v|.
+  // The tables are written with a guess (the prefix's exponent, at least 0), which is right
+  // unless that V lies outside [2^-6, 2^13) or the prefix's exponent is negative; then they are
+  // written again behind one more barrier (the same decision in every wave).
+  const int Up = U;   // kNoExp without a prefix
+  U = max(Up, 0);
+  if (Up != kNoExp && U != Up) acc_scale<NB>(S, __builtin_ldexpf(1.0f, Up - U));
   init_kt_constants(L.KT, tid, 64 * NWAVE_OUT);
   publish_state<NB>(L, S, OB::first, r, h);
   if (GRAM) publish_gram(L, G, r, h);
-  stage_convert<true>(st, cv, p.alpha, p.beta, lane);
+  stage_convert_qk<true>(st, cv, p.qs, p.ks, lane);
+  if (U == 0)
+    stage_convert_v(st, cv);
+  else
+    stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -U));
   stage_write<true>(cv, L.Q0, L.Kr, L.KT, L.VT, lane, W);
+  {
+    const u32 mvk = wave_max_u16x2((stage_vmax(st) << 16) | stage_kmax(st));
+    if (lane == 0) {
+      L.xv[0][W] = mvk >> 16;
+      L.xk[0][W] = mvk & 0xffffu;
+    }
+  }
   lds_barrier();
+  // the current chunk's max |v| and |k| exponents, for the bound on its state increment
+  int eVc = exp_of_f32bits(lds_max4(L.xv[0]) << 16);
+  int eKc = exp_of_f32bits(lds_max4(L.xk[0]) << 16);
+  {
+    const int U0 = max(Up, first_unit(eVc));
+    if (U0 != U) {   // rare, and the same in every wave
+      acc_scale<NB>(S, __builtin_ldexpf(1.0f, U - U0));
+      U = U0;
+      publish_state<NB>(L, S, OB::first, r, h);
+      stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -U));
+      stage_write_v(cv, L.VT, lane, W);
+      lds_barrier();
+    }
+  }
 
   constexpr u32 kOnes = 0x3c003c00u;
   for (int c = 0; c < nch; ++c) {
     const int row0 = (c0 + c) * CH;
+    // max |S| of the state this chunk starts from (its MFMAs have completed: it was published)
+    const u32 msS = wave_max_u32(acc_absmax<NB>(S));
     // next chunk, issued unconditionally (one basic block); after the last chunk it reads nothing
     stage_load<VEC, true>(st, p, qh, kh, vh, min(row0 + CH, N - 1), lane, W, c + 1 < nch);
 
@@ -778,18 +1053,19 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
       dden = __builtin_fmaf(T[5], f16_hi_to_f32(qy[0]), dden);
       dden = __builtin_fmaf(T[6], f16_lo_to_f32(qy[1]), dden);
       dden = __builtin_fmaf(T[7], f16_hi_to_f32(qy[1]), dden);
+      dden *= __builtin_ldexpf(1.0f, __builtin_amdgcn_readfirstlane(L.eg));
     }
 
-    // ---- intra-chunk: key tiles j <= W
+    // ---- intra-chunk: key tiles j <= W; scores b/2 = 1/2 + q~.(k~/2), P = (b/2)^2 + 1/4 = p/2
     float rs = 0.f;
 #pragma unroll
     for (int j = 0; j <= W; ++j) {
       const u32x4 ka = *reinterpret_cast<const u32x4*>(&L.Kr[(32 * j + perm32(r)) * QRS + 8 * h]);
-      const f32x16 sc = mfma32x32x16_f16(ka, qb, splat16(1.0f));
+      const f32x16 sc = mfma32x32x16_f16(ka, qb, splat16(0.5f));
       u32 pk[8];
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
-        pk[x] = pack_f16x2(__builtin_fmaf(sc[2 * x], sc[2 * x], 1.0f), __builtin_fmaf(sc[2 * x + 1], sc[2 * x + 1], 1.0f));
+        pk[x] = pack_f16x2(__builtin_fmaf(sc[2 * x], sc[2 * x], 0.25f), __builtin_fmaf(sc[2 * x + 1], sc[2 * x + 1], 0.25f));
         if (j == W) pk[x] &= dmask[x];
         rs = dot2_f16(pk[x], kOnes, rs);
       }
@@ -805,13 +1081,14 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
     }
 
     // ---- normaliser and outputs.  Lane (token 32W + r, half h) holds dv 32n + 8jj + 4h + i
-    // in O[n][4jj + i]; all values are in units of 2p.
+    // in O[n][4jj + i]; O is num / 2 in units of 2^U, dden and rs are sums of p/2 - 1/2 and p/2.
     {
       float x = dden + rs;
       x += __shfl_xor(x, 32);
-      const float den = (float)row0 + p.prev_tokens + 0.5f * x;
+      const float den = (float)row0 + p.prev_tokens + 2.0f * x;
+      const float un = __builtin_ldexpf(2.0f, U);
       // v_rcp_f32 (1 ulp) instead of an IEEE division, and a select, keep this branch-free
-      const float sc = p.normalize ? 0.5f * __builtin_amdgcn_rcpf(den + p.eps) : 0.5f;
+      const float sc = p.normalize ? un * __builtin_amdgcn_rcpf(den + p.eps) : un;
       const int row = row0 + 32 * W + r;
       if (VEC) {
         const __amdgpu_buffer_rsrc_t ro =
@@ -855,16 +1132,55 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
     // ---- state update with this chunk
     update_blocks<NB>(L.KT, L.VT, S, ra, rb, r, h);
     if (GRAM) gram_update(L.KT, G, grow, h, 0, 1);
-    stage_convert<true>(st, cv, p.alpha, p.beta, lane);   // next chunk, in registers
+    const bool more = c + 1 < nch;
+    // next chunk in registers (V with the current exponent), and the maxima that decide the
+    // next exponent: |S| before this update, |v| and |k| of the next chunk
+    stage_convert_qk<true>(st, cv, p.qs, p.ks, lane);
+    stage_convert_v(st, cv);   // exponent 0; the rare path below converts again otherwise
     stage_pin<true>(cv);
+    {
+      const int par = (c + 1) & 1;
+      const u32 mvk = wave_max_u16x2(more ? (stage_vmax(st) << 16) | stage_kmax(st) : 0u);
+      if (lane == 0) {
+        L.xs[par][W] = msS;
+        L.xv[par][W] = mvk >> 16;
+        L.xk[par][W] = mvk & 0xffffu;
+      }
+    }
 
     lds_barrier();   // every wave is done with this chunk's tables and the published state
-    if (c + 1 < nch) {
+    if (more) {
       stage_write<true>(cv, L.Q0, L.Kr, L.KT, L.VT, lane, W);
       publish_state<NB>(L, S, OB::first, r, h);
       if (GRAM) publish_gram(L, G, r, h);
-      lds_barrier();
     }
+    {
+      // The state just published is below its max before this update plus a bound on this
+      // chunk's increment, 128 max|k-side product| max|v 2^-U| (the table products are
+      // (k~/2)^2-sized, k~/4 or 1/2); if that bound or the next chunk's V would leave fp16 the
+      // exponent rises and the rare path rewrites what was just written (before the barrier).
+      const int par = (c + 1) & 1;
+      const int eS = exp_of_f32bits(lds_max4(L.xs[par]));
+      const int eV = exp_of_f32bits(lds_max4(L.xv[par]) << 16);
+      const int eK = exp_of_f32bits(lds_max4(L.xk[par]) << 16);
+      const float kk = eKc == kNoExp ? 0.f : p.ks * __builtin_ldexpf(2.0f, eKc);
+      const float kf = __builtin_fmaxf(kk * kk, __builtin_fmaxf(0.5f * kk, 0.5f));
+      const float dS = eVc == kNoExp ? 0.f : 128.0f * kf * __builtin_ldexpf(2.0f, eVc - U);
+      const float sb = (eS == kNoExp ? 0.f : __builtin_ldexpf(2.0f, eS)) + dS;
+      const int Un = next_unit(U, exp_of_f32bits(__builtin_bit_cast(u32, sb)), eV);
+      if (Un != U || (Un != 0 && more)) {   // rare, and the same in every wave
+        if (Un != U) acc_scale<NB>(S, __builtin_ldexpf(1.0f, U - Un));
+        if (more) {
+          stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -Un));
+          stage_write_v(cv, L.VT, lane, W);
+          if (Un != U) publish_state<NB>(L, S, OB::first, r, h);
+        }
+        U = Un;
+      }
+      eVc = eV;
+      eKc = eK;
+    }
+    if (more) lds_barrier();
   }
 
   // ---- final state of the head (last segment) in the reference feature basis, fp32:
@@ -878,6 +1194,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
       for (int e = 0; e < 16; ++e) G32[(8 * (e >> 2) + 4 * h + (e & 3)) * 33 + r] = G[e];
     }
     lds_barrier();
+    const float su = __builtin_ldexpf(4.0f, U);   // state registers -> k side of 2p
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int blk = OB::first + b;
@@ -887,7 +1204,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
         const int f = 32 * blk + 16 * (e >> 3) + 8 * h + (e & 7);
         const RefFeat rf = ref_feature(f);
         if (rf.ref < 0) continue;
-        const float fac = p.st_fac[rf.fac];
+        const float fac = p.st_fac[rf.fac] * su;
 #pragma unroll
         for (int n = 0; n < 2; ++n) {
           const int col = 32 * n + r;
@@ -903,7 +1220,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
         float fa, fb;
         kt_row_dim(kr.a, da, fa);
         kt_row_dim(kr.b, db, fb);
-        const float z = fa * fb * G32[da * 33 + db];
+        const float z = 4.0f * fa * fb * G32[da * 33 + db];
         so[(size_t)rf.ref * (dv + 1) + dv] = rf.ref == 0 ? (float)N + p.prev_tokens : z * p.st_fac[rf.fac];
       }
     }
@@ -943,7 +1260,8 @@ size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk) {
   if (d != 16 || dv > 64 || chunk < 1) return (size_t)-1;
   int P, seg_chunks;
   segment_split(BH, N, P, seg_chunks);
-  const size_t per = (size_t)64 * NF * 2 + (size_t)1024 * 4;
+  // per (head, segment): fp16 S^T, fp32 Gram matrix, two exponents
+  const size_t per = (size_t)64 * NF * 2 + (size_t)1024 * 4 + 2 * sizeof(int);
   return (size_t)BH * P * per + 256;
 }
 
@@ -972,23 +1290,21 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
   segment_split(a.BH, a.N, P, seg_chunks);
   p.P = P;
   p.seg_chunks = seg_chunks;
-  const size_t sS = (size_t)a.BH * P * 64 * NF * 2;
+  const size_t nslot = (size_t)a.BH * P;
   char* ws = static_cast<char*>(a.workspace);
   p.wsS = reinterpret_cast<uint16_t*>(ws);
-  p.wsG = reinterpret_cast<float*>(ws + sS);
-  // q~ = alpha q, k~ = beta k with alpha beta = scale; sigma moves magnitude from the state
-  // (sums over up to N tokens) to the q side so that it stays well inside the fp16 range.
-  int sigma = 0;
-  const double total = (double)a.N + (double)a.prev_tokens;   // tokens the state will sum over
-  while ((double)(1 << (sigma + 10)) < total && sigma < 12) sigma += 2;
+  p.wsG = reinterpret_cast<float*>(ws + nslot * 64 * NF * 2);
+  p.wsE = reinterpret_cast<int*>(ws + nslot * (64 * NF * 2 + 1024 * 4));
+  p.wsEP = p.wsE + nslot;
+  // q~ = sqrt(scale) q (q~.k~ = s); the K^T table rows hold k~/2
   const double rc = sqrt((double)a.scale);
-  p.alpha = (float)(rc * ldexp(1.0, sigma / 2));
-  p.beta = (float)(rc * ldexp(1.0, -sigma / 2));
-  // internal k side -> reference features: constant 2, linear k~, square k~^2, pair k~ k~
+  p.qs = (float)rc;
+  p.ks = (float)(0.5 * rc);
+  // k side of 2p -> reference features: constant 2, linear k~, square k~^2, pair k~ k~
   p.st_fac[0] = 0.5f;
-  p.st_fac[1] = (float)ldexp(1.0, sigma / 2);
-  p.st_fac[2] = (float)(ldexp(1.0, sigma) / sqrt(2.0));
-  p.st_fac[3] = (float)ldexp(1.0, sigma);
+  p.st_fac[1] = 1.0f;
+  p.st_fac[2] = (float)(1.0 / sqrt(2.0));
+  p.st_fac[3] = 1.0f;
   for (int i = 0; i < 4; ++i) p.st_inv[i] = (float)(1.0 / (double)p.st_fac[i]);
   p.state_in = a.state_in;
   p.prev_tokens = (float)a.prev_tokens;

@@ -10,10 +10,13 @@
 // (benchmarks/chunked_attention_benchmark.py:34-53) evaluated through the exact identity
 // phi(q).phi(k) = 1 + s + s^2/2, so phi is never materialised.
 //
-// Precision.  The P.V product runs as an fp16 MFMA: V is converted bf16 -> fp16 (exact for
-// 2^-14 <= |v| <= 65504) and u is rounded to fp16 (2^-11 relative, 8x finer than bf16).  Q is
-// pre-scaled by 2^-k (exact) so that the rounded quantity is u * 2^-2k ~ r and stays far from
-// fp16 overflow (|q.k| * scale < ~255).  The constant 1 of p is kept exact:
+// Precision and range.  The P.V product runs as an fp16 MFMA: V is converted bf16 -> fp16 after
+// a power-of-two scale 2^-E chosen per head from max |v| (so any bf16 magnitude lands in fp16's
+// normal range; the accumulators are multiplied by 2^E at the end), and u is rounded to fp16
+// (2^-11 relative, 8x finer than bf16).  Q is pre-scaled by 2^-k (exact) so that the rounded
+// quantity is W r with W = 2^-2k 2/c^2 in (0.18, 0.71] (1/2 at scale = 1/4): r = s + s^2/2 may
+// reach 65504 / W, i.e. |s| = |q.k| * scale up to about 430 (511 at W = 1/2), where bf16's own
+// p = 1 + s + s^2/2 is 1.3e5.  The constant 1 of p is kept exact:
 //   * key blocks strictly before the wave's queries contribute sum(v) through fp32 column sums
 //     of V: computed by the pre-pass and prefix-summed over blocks (packed path), or kept as a
 //     running sum in the key loop (v_dot2 against packed ones) and snapshotted per wave;
@@ -40,6 +43,7 @@
 // Other shapes stage K and V through registers into a double-buffered LDS block.
 #include <type_traits>
 
+#include "../../include/based_la.h"
 #include "la_common.hpp"
 #include "la_internal.hpp"
 #include "la_pack.hpp"
@@ -75,8 +79,11 @@ struct ParallelParams {
   float inv_c, inv_c2, fscale, eps;
   float qscale;           // 2^-k applied to q (exact in bf16)
   u32 ones_hi, ones_lo;   // fp16 bits of the weight W of "1" in u units, hi + lo (both halves)
+  const u32* vmax;        // register-staged bf16 path: per head, VR partial maxima of |v| (bf16 bits)
   int normalize, out_f32;
 };
+
+constexpr int VR = 64;    // partial maxima of |v| per head (vrange_kernel)
 
 constexpr int NRAW = 7;   // LDS stages of the packed path
 
@@ -87,8 +94,8 @@ size_t vt_block_bytes(int dv) { return dv <= 32 ? (size_t)VtBlockP<32>::bytes : 
 
 bool packed_shape(int d, int dv) { return d == 16 && dv % 8 == 0 && dv <= 64; }
 
-// UNIT: 1/c scales to exactly 1 (scale = 1/sqrt(d) with d a power of 4), so the score MFMA
-// starts from the inline constant 1.0 and u = b*b - 1.
+// UNIT: 1/c scales to exactly 1/2 (scale = 1/sqrt(d) with d a power of 4), so the score MFMA
+// starts from the inline constant 0.5 and u = b*b - 1/4.
 //
 // NW waves per work-group (4, or 8 on the packed path, where the registers are capped so that
 // four waves share each SIMD).
@@ -165,7 +172,9 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) rsum[qt] = 0.f;
 
-  const float inv_c = UNIT ? 1.0f : p.inv_c, inv_c2 = UNIT ? 1.0f : p.inv_c2;
+  const float inv_c = UNIT ? 0.5f : p.inv_c, inv_c2 = UNIT ? 0.25f : p.inv_c2;
+  // V exponent E of this head: V^T holds fp16(V 2^-E); vexp_f = 2^E
+  float vexp_f = 1.0f;
 
   // running column sum of V over blocks [0, jb0 + s) for snapshot s: thread -> (row, segment)
   const int vs_row = tid / LPR, vs_seg = tid % LPR;
@@ -334,6 +343,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       qf[qt][0] = scale_bf16x8(*reinterpret_cast<const u32x4*>(qs + (32 * qt + n) * 16 + 8 * h), p.qscale);
     const float* rec = reinterpret_cast<const float*>(region + 4096 + 512 * wu);
     if (lane < DV) vsl[wu][lane] = rec[lane];   // column sums of V, for the epilogue
+    vexp_f = __builtin_ldexpf(1.0f, (int)rec[DV + kStatExpH]);
     if (wave_live) {
       // Row sums of u over the blocks before the diagonal block, x = q~ (the query's 16 dims):
       // x^T U x + (2/c) x.k1 with U the k k^T prefix as an upper-triangular matrix (off-diagonal
@@ -382,6 +392,11 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
     }
     lds_barrier();
   } else {
+    // the head's V exponent from the VR partial maxima of vrange_kernel
+    const u32 m = wave_max_u32(lane < VR ? p.vmax[(size_t)bh * VR + lane] : 0u);
+    const int E = vexp_step(m << 16);
+    st.vscale = __builtin_ldexpf(1.0f, -E);
+    vexp_f = __builtin_ldexpf(1.0f, E);
     st.load(kg, vg, 0, N, d, dv, tid);
     st.store(Ks[0], VTs[0], tid);
     if (jb0 == 0) snap[0][tid] = 0.f;
@@ -620,6 +635,9 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
     }
 
   const float fscale = p.fscale;
+  // packed: acc in units of 2^E, vsum exact fp32; register-staged: both in units of 2^E
+  const float afs = PACKED ? fscale * vexp_f : fscale;
+  const float ofs = PACKED ? 1.0f : vexp_f;
   if (PACKED) {
     // The wave's output tile (32 QT queries x DV) goes through its own part of the free stages so
     // that the stores write whole rows: lane -> (row, 16-byte chunk).
@@ -641,7 +659,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
           for (int g = 0; g < 4; ++g) {
             float y[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = (fscale * acc[qt][mt][4 * g + e] + vsum[mt][4 * g + e]) * inv;
+            for (int e = 0; e < 4; ++e) y[e] = (afs * acc[qt][mt][4 * g + e] + vsum[mt][4 * g + e]) * inv;
             char* dst = tile + (32 * qt + n) * RS + (32 * mt + 8 * g + 4 * h) * EB;
             if (F32)
               *reinterpret_cast<f32x4*>(dst) = (f32x4){y[0], y[1], y[2], y[3]};
@@ -670,7 +688,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
     const int query = wq0 + 32 * qt + n;
     if (query >= N) continue;
     const float den = (float)(query + 1) + fscale * rs;
-    const float inv = p.normalize ? 1.0f / (den + p.eps) : 1.0f;
+    const float inv = (p.normalize ? 1.0f / (den + p.eps) : 1.0f) * ofs;
     if (p.den != nullptr && h == 0) p.den[hrow + query] = den;
     const size_t obase = (hrow + query) * (size_t)dv;
 #pragma unroll
@@ -680,7 +698,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
         const int col = 32 * mt + 8 * g + 4 * h;
         float y[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = (fscale * acc[qt][mt][4 * g + e] + vsum[mt][4 * g + e]) * inv;
+        for (int e = 0; e < 4; ++e) y[e] = (afs * acc[qt][mt][4 * g + e] + vsum[mt][4 * g + e]) * inv;
         if (VEC) {
           if (col < dv) {
             if (p.out_f32) {
@@ -707,6 +725,25 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
 }
 
 
+// Partial maxima of |v| for the register-staged bf16 kernel: work-group (s, bh) takes rows
+// [s R, (s + 1) R) of head bh, R = ceil(N / VR), and writes the largest bf16 magnitude (as bits)
+// to vmax[bh][s]; the main kernel reduces the VR partials of its head to the V exponent.
+__global__ __launch_bounds__(256) void vrange_kernel(const uint16_t* __restrict__ v, int N, int dv,
+                                                     u32* __restrict__ vmax) {
+  __shared__ u32 wm[4];
+  const int tid = threadIdx.x, s = blockIdx.x, bh = blockIdx.y;
+  const int R = (N + VR - 1) / VR;
+  const int r0 = min(N, s * R), r1 = min(N, r0 + R);
+  const uint16_t* base = v + ((size_t)bh * N + r0) * dv;
+  const long long n = (long long)(r1 - r0) * dv;
+  u32 m = 0u;
+  for (long long i = tid; i < n; i += 256) m = max(m, (u32)(base[i] & 0x7fffu));
+  m = wave_max_u32(m);
+  if ((tid & 63) == 0) wm[tid >> 6] = m;
+  __syncthreads();
+  if (tid == 0) vmax[(size_t)bh * VR + s] = max(max(wm[0], wm[1]), max(wm[2], wm[3]));
+}
+
 // Packed path: pre-pass, column-sum scan, then the main kernel with 4 waves x 32 QT queries (8
 // waves x 32 queries at four waves per SIMD measured slower).
 template <int MT, int QT>
@@ -720,11 +757,12 @@ int launch_packed(const ParallelParams& pp, int stages, hipStream_t stream) {
                        stream, p.k, p.v, const_cast<uint16_t*>(p.vt), const_cast<float*>(p.stats), p.N, p.dv,
                        p.nb64);
     hipLaunchKernelGGL(stats_scan_kernel, dim3((unsigned)p.BH, (unsigned)(stats_width(DV) / 16)), dim3(256), 0,
-                       stream, const_cast<float*>(p.stats), p.nb64, stats_width(DV));
+                       stream, const_cast<float*>(p.stats), p.nb64, stats_width(DV), DV + kStatExpB,
+                       const_cast<uint16_t*>(p.vt), VtBlockP<DV>::bytes / 2);
   }
   if (stages & 2) {
     const dim3 grid((unsigned)(p.nqb * p.BH)), block(64 * NW);
-    const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
+    const bool unit = p.inv_c == 0.5f && p.inv_c2 == 0.25f;
     if (unit)
       hipLaunchKernelGGL((based_parallel_bf16_kernel<1, MT, QT, true, true, true, NW>), grid, block, 0, stream, p);
     else
@@ -745,12 +783,17 @@ int launch_bf16(const ParallelParams& pp, bool vec, bool packed, int stages, hip
                                                                  : launch_packed<MT, 1>(pp, stages, stream);
     }
   }
-  if (!(stages & 2)) return 0;
+  if (stages & 1) {
+    // per-head |v| maxima for the V exponent of the register-staged kernel
+    hipLaunchKernelGGL(vrange_kernel, dim3((unsigned)VR, (unsigned)pp.BH), dim3(256), 0, stream, pp.v, pp.N, pp.dv,
+                       const_cast<u32*>(pp.vmax));
+  }
+  if (!(stages & 2)) return (int)hipGetLastError();
   constexpr int BM = 128 * QT;
   ParallelParams p = pp;
   p.nqb = (p.N + BM - 1) / BM;
   const dim3 grid((unsigned)(p.nqb * p.BH)), block(256);
-  const bool unit = p.inv_c == 1.0f && p.inv_c2 == 1.0f;
+  const bool unit = p.inv_c == 0.5f && p.inv_c2 == 0.25f;
   if (vec && unit)
     hipLaunchKernelGGL((based_parallel_bf16_kernel<KS, MT, QT, true, true, false, 4>), grid, block, 0, stream, p);
   else if (vec)
@@ -770,9 +813,17 @@ int dispatch_mt(const ParallelParams& p, bool vec, bool packed, int stages, hipS
 
 }  // namespace
 
-// [V^T blocks: BH * nb64 * vt_block_bytes][statistics prefixes: BH * nb64 * stats_width(DV) fp32]
+// bf16 inputs.  Packed shapes: [V^T blocks: BH * nb64 * vt_block_bytes][statistics prefixes:
+// BH * nb64 * stats_width(DV) fp32].  Other shapes: BH * VR partial maxima of |v| (u32).  The
+// packed layout is never smaller, so a packed shape that falls back to the register-staged
+// kernel (misaligned tensors) keeps its partial maxima at the start of the same workspace.
+size_t vrange_bytes(int BH) { return (size_t)BH * VR * 4; }
+
+bool parallel_packed_shape(int d, int dv, bool in_f32) { return !in_f32 && packed_shape(d, dv); }
+
 size_t parallel_workspace_bytes(int BH, int N, int d, int dv, bool in_f32) {
-  if (in_f32 || !packed_shape(d, dv)) return 0;
+  if (in_f32) return 0;
+  if (!packed_shape(d, dv)) return vrange_bytes(BH);
   const size_t nb64 = ((size_t)N + BN - 1) / BN;
   const int DV = dv <= 32 ? 32 : 64;
   return (size_t)BH * nb64 * (vt_block_bytes(dv) + (size_t)stats_width(DV) * 4);
@@ -787,6 +838,7 @@ int launch_based_parallel(const ParallelArgs& a, hipStream_t stream) {
   p.k = static_cast<const uint16_t*>(a.k);
   p.v = static_cast<const uint16_t*>(a.v);
   p.vt = static_cast<const uint16_t*>(a.workspace);
+  p.vmax = static_cast<const u32*>(a.workspace);
   p.nb64 = (a.N + BN - 1) / BN;
   if (a.workspace != nullptr)
     p.stats = reinterpret_cast<const float*>(static_cast<const char*>(a.workspace) +
@@ -797,10 +849,11 @@ int launch_based_parallel(const ParallelArgs& a, hipStream_t stream) {
   p.N = a.N;
   p.d = a.d;
   p.dv = a.dv;
-  // Work in u'' = 2^-2k u with u = (q.k + 1/c)^2 - 1/c^2 = (2/c^2) r, k chosen so the weight of
-  // "1", W = 2^-2k * 2/c^2, is close to 1 (u'' ~ r).
+  // Work in u'' = 2^-2k u with u = (q.k + 1/c)^2 - 1/c^2 = (2/c^2) r, k chosen so that the weight
+  // of "1", W = 2^-2k * 2/c^2, lies in (0.18, 0.71] (u'' = W r): r up to 65504 / W stays inside
+  // fp16 (|s| up to ~430, 511 at scale = 1/4, where W = 1/2 and 1/c scales to 1/2).
   const double ic = 1.0 / (double)a.scale;
-  const int k = (int)__builtin_lround(0.5 * __builtin_log2(2.0 * ic * ic) - 0.25);
+  const int k = (int)__builtin_lround(0.5 * __builtin_log2(2.0 * ic * ic) + 0.75);
   const double qs = __builtin_ldexp(1.0, -k);
   const float icf = (float)(ic * qs);
   p.qscale = (float)qs;
@@ -821,7 +874,8 @@ int launch_based_parallel(const ParallelArgs& a, hipStream_t stream) {
                    ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0);
   // packed path: the shape takes it, the workspace is there, and the sizes fit the 32-bit
   // buffer offsets.  The caller checked alignment (packed_alignment_ok).
-  const bool packed = packed_shape(a.d, a.dv) && a.workspace != nullptr &&
+  if (a.workspace == nullptr || a.workspace_bytes < vrange_bytes(a.BH)) return LA_ERR_WORKSPACE;
+  const bool packed = packed_shape(a.d, a.dv) && a.packed_aligned &&
                       a.workspace_bytes >= parallel_workspace_bytes(a.BH, a.N, a.d, a.dv, false) &&
                       (size_t)p.nb64 * vt_block_bytes(a.dv) < ((size_t)1 << 30) && (size_t)a.N * 32 < ((size_t)1 << 30);
   if (a.d <= 16) return dispatch_mt<1>(p, vec, packed, a.stages, stream);

@@ -80,18 +80,22 @@ int parallel_entry(const void* q, const void* k, const void* v, int in_dtype, vo
   const size_t need = la::parallel_workspace_bytes(B * H, N, d, dv, in_dtype == LA_F32);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
   if (need > 0 && !al(workspace, 16)) return LA_ERR_BAD_ALIGNMENT;
-  // the packed kernels copy q, k, v^T rows 16 bytes at a time and store out 8 bytes at a time
+  // the packed kernels copy q, k, v^T rows 16 bytes at a time and store out 8 bytes at a time;
+  // misaligned tensors of a packed shape run the register-staged kernel, which needs the
+  // pre-pass and the main kernel in one call
   const bool aligned = al(q, 16) && al(k, 16) && al(v, 8) && al(out, 16);
-  if (need > 0 && stages != 3 && !aligned) return LA_ERR_BAD_ALIGNMENT;
+  if (la::parallel_packed_shape(d, dv, in_dtype == LA_F32) && stages != 3 && !aligned) return LA_ERR_BAD_ALIGNMENT;
   la::ParallelArgs a{};
   a.q = q;
   a.k = k;
   a.v = v;
   a.out = out;
   a.den = den_or_null;
-  a.workspace = (need > 0 && aligned) ? workspace : nullptr;
-  a.workspace_bytes = (need > 0 && aligned) ? workspace_bytes : 0;
-  a.stages = a.workspace != nullptr ? stages : (stages & 2 ? 3 : 0);
+  a.workspace = need > 0 ? workspace : nullptr;
+  a.workspace_bytes = need > 0 ? workspace_bytes : 0;
+  a.packed_aligned = aligned;
+  // fp32 inputs have no pre-pass: a pack-only call does nothing, a main-only call is the whole call
+  a.stages = need > 0 ? stages : (stages & 2 ? 3 : 0);
   a.BH = B * H;
   a.N = N;
   a.d = d;

@@ -293,7 +293,7 @@ int launch_identity_t(IdentityParams p, hipStream_t stream) {
   const dim3 grid((unsigned)p.ns, (unsigned)p.BH), block(64 * kIdNW);
   hipLaunchKernelGGL((identity_kernel<KS, MT, true>), grid, block, 0, stream, p);
   hipLaunchKernelGGL(stats_scan_kernel, dim3((unsigned)p.BH, (unsigned)(32 * MT * 16 * KS / 16)), dim3(256), 0, stream,
-                     p.state, p.ns, 32 * MT * 16 * KS);
+                     p.state, p.ns, 32 * MT * 16 * KS, 32 * MT * 16 * KS, nullptr, 0);
   hipLaunchKernelGGL((identity_kernel<KS, MT, false>), grid, block, 0, stream, p);
   return (int)hipGetLastError();
 }

@@ -119,6 +119,20 @@ __device__ __forceinline__ f32x16 splat16(float x) {
   return r;
 }
 
+// Wave-wide maximum of an unsigned value (fp32 magnitudes order as their bits), returned in
+// every lane: a running maximum along each row of 16 lanes (DPP row_shr 1, 2, 4, 8), then rows
+// 0-1 and 2-3 joined by row_bcast15 and all four by row_bcast31, read from lane 63.  Lanes
+// whose DPP source lies outside the row take 0, which leaves a maximum of unsigned values alone.
+__device__ __forceinline__ u32 wave_max_u32(u32 x) {
+  x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xf, 0xf, false));   // row_shr:1
+  x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xf, 0xf, false));   // row_shr:2
+  x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xf, 0xf, false));   // row_shr:4
+  x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xf, 0xf, false));   // row_shr:8
+  x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));   // row_bcast:15
+  x = max(x, (u32)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));   // row_bcast:31
+  return (u32)__builtin_amdgcn_readlane((int)x, 63);
+}
+
 // Row (key / dv index) of element i of a 32x32 accumulator held by lane group h.
 __device__ __forceinline__ int c32_row(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
 

@@ -14,8 +14,9 @@ struct ParallelArgs {
   const void* v;
   void* out;
   float* den;          // optional, (BH, N) fp32, den without eps
-  void* workspace;     // optional scratch of parallel_workspace_bytes(); enables the packed path
+  void* workspace;     // parallel_workspace_bytes() of scratch (bf16 inputs)
   size_t workspace_bytes;
+  bool packed_aligned; // q, k, out 16-byte and v 8-byte aligned: the packed kernels may run
   int stages;          // packed path: 1 = pre-pass (pack V), 2 = main kernel, 3 = both
   int BH, N, d, dv;
   float scale, eps;
@@ -85,6 +86,7 @@ struct FeatureMapArgs {
 // and returns 0, a negative LA_ERR_* code, or a positive hipError_t.
 int launch_based_parallel(const ParallelArgs& a, hipStream_t stream);
 size_t parallel_workspace_bytes(int BH, int N, int d, int dv, bool in_f32);
+bool parallel_packed_shape(int d, int dv, bool in_f32);   // shapes of the packed (pre-pass) kernel
 int launch_sliding_window(const SlidingArgs& a, hipStream_t stream);
 size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk);
 int chunked_chunk_tokens();   // tokens per chunk of the chunked kernels

@@ -3,9 +3,19 @@
 //    so that the main kernel copies a block straight into LDS with buffer_load ... lds;
 //  * the block's statistics, a record of stats_width(DV) floats: the column sums of V (DV), the
 //    sums of k (16) and the upper triangle of sum k k^T (136 entries, row-major, off-diagonal
-//    entries doubled), then zero padding.  A scan turns the records into exclusive prefixes over
-//    the blocks, from which the main kernel takes everything a query needs of the blocks before
-//    its diagonal block except the P.V products themselves.
+//    entries doubled), then eight words: the block's V exponent, the head's V exponent, zeros.
+//    A scan turns the sums into exclusive prefixes over the blocks, from which the main kernel
+//    takes everything a query needs of the blocks before its diagonal block except the P.V
+//    products themselves.
+//
+// Range of V.  fp16 holds 2^-14 .. 65504 (normal), bf16 2^-126 .. 3.4e38, so V^T is stored as
+// fp16(V * 2^-E) with E a multiple of 8 chosen per head: every block first takes the exponent
+// e_b = vexp_step(max |v| of the block), which puts the block's largest |v'| in [1/2, 128); the
+// scan then sets the head's E = max_b e_b and multiplies the V^T blocks with e_b < E by
+// 2^(e_b - E) in place (exact, or the rounding of a direct conversion when values fall below
+// 2^-14).  For V of one order of magnitude every block has the same e_b and nothing is rewritten.
+// The main kernel multiplies its P.V accumulators by 2^E.  The column sums of V stay fp32 sums
+// of the unscaled bf16 values.
 #pragma once
 
 #include "la_common.hpp"
@@ -23,7 +33,18 @@ struct VtBlock {
 constexpr int kStatK1 = 0;     // offset of the k sums after the V column sums
 constexpr int kStatK2 = 16;    // offset of the k k^T triangle after the V column sums
 constexpr int kTri = 136;      // entries of the triangle (16 * 17 / 2)
+constexpr int kStatExpB = kStatK2 + kTri;       // the block's V exponent (float), not prefix-summed
+constexpr int kStatExpH = kStatK2 + kTri + 1;   // the head's V exponent, written by the scan
 __host__ __device__ constexpr int stats_width(int DV) { return DV + 160; }
+
+// Power-of-two step (a multiple of 8) of a V block or head from the bits of max |v| as an fp32
+// value: 8 ceil((e - 6) / 8) for max |v| in [2^e, 2^(e+1)), so max |v| * 2^-step lies in
+// [1/2, 128); -128 for an all-zero block (below every other step).
+__device__ __forceinline__ int vexp_step(u32 absmax_f32_bits) {
+  if (absmax_f32_bits == 0u) return -128;
+  const int e = (int)(absmax_f32_bits >> 23) - 127;   // subnormal fp32 (from bf16) -> -127
+  return 8 * ((e + 1) >> 3);
+}
 
 // One work-group per PPW consecutive 64-key blocks of a head (all their loads issued first); k
 // rows are d = 16 bf16 (16-byte aligned), v rows dv % 8 == 0 bf16 (8-byte aligned).  Per block:
@@ -49,6 +70,7 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
   __shared__ __attribute__((aligned(16))) u32 img[IMG / 4];
   __shared__ __attribute__((aligned(16))) uint16_t kl[BN * 16];
   __shared__ float csum[NWV][DV];
+  __shared__ u32 vmx[4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int bh = blockIdx.y, blk0 = blockIdx.x * PPW;
   const int nb = min(PPW, nb64 - blk0);
@@ -84,7 +106,20 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
   for (int b = 0; b < PPW; ++b) {
     if (b >= nb) break;
     const int blk = blk0 + b;
-    __syncthreads();   // image zeroed / the previous block's readers done
+    {
+      // max |v| of the block: bf16 magnitudes compare as integers; per wave, then through LDS
+      u32 m = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32 x = va[b][i] & 0x7fff7fffu, y = vb[b][i] & 0x7fff7fffu;
+        m = max(m, max(max(x & 0xffffu, x >> 16), max(y & 0xffffu, y >> 16)));
+      }
+      m = wave_max_u32(m);
+      if (lane == 0) vmx[w] = m;
+    }
+    __syncthreads();   // image zeroed / the previous block's readers done / wave maxima written
+    const int eb = vexp_step(max(max(vmx[0], vmx[1]), max(vmx[2], vmx[3])) << 16);
+    const float vs = __builtin_ldexpf(1.0f, -eb);
     float part[8];
     if (tid < NT) {
 #pragma unroll
@@ -93,7 +128,7 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
         const float f0 = (e & 1) ? bf16_hi_to_f32(a0) : bf16_lo_to_f32(a0);
         const float f1 = (e & 1) ? bf16_hi_to_f32(a1) : bf16_lo_to_f32(a1);
         part[e] = f0 + f1;
-        img[(col + e) * (ROW / 2) + kp] = pack_f16x2(f0, f1);
+        img[(col + e) * (ROW / 2) + kp] = pack_f16x2(f0 * vs, f1 * vs);
       }
     } else {
 #pragma unroll
@@ -142,19 +177,26 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
         if (nn < 16 && a <= nn) rec[DV + kStatK2 + 16 * a - a * (a - 1) / 2 + nn - a] = a == nn ? acc[i] : 2.f * acc[i];
         if (nn == 16) rec[DV + kStatK1 + a] = acc[i];
       }
-      if (lane < 8) rec[DV + kStatK2 + kTri + lane] = 0.f;
+      if (lane < 8) rec[DV + kStatK2 + kTri + lane] = lane == 0 ? (float)eb : 0.f;
     }
   }
 }
 
-// stats[bh][blk][sw] -> exclusive prefix over blk, in place.  Work-group (bh, g) scans columns
+// stats[bh][blk][sw] -> exclusive prefix over blk, in place, of columns [0, nsum); the columns
+// from nsum on (the exponent words) are left alone.  Work-group (bh, g) scans columns
 // 16 g .. 16 g + 15 of head bh in tiles of 256 blocks: 16 threads per column each sum a run of 16
 // blocks, a 16-term scan of the run totals gives each run's offset, and a carry links the tiles.
-__global__ __launch_bounds__(256) void stats_scan_kernel(float* __restrict__ stats, int nb64, int sw) {
+// With vt set (the packed parallel pre-pass), the work-group of the last column group then
+// settles the head's V exponent (vt_head_exponent); other users scan every column (nsum = sw).
+__device__ void vt_head_exponent(float* __restrict__ s, uint16_t* __restrict__ vt, int nb64, int sw, int vt_halves);
+
+__global__ __launch_bounds__(256) void stats_scan_kernel(float* __restrict__ stats, int nb64, int sw, int nsum,
+                                                         uint16_t* __restrict__ vt, int vt_halves) {
   constexpr int CW = 16, NT = 256 / CW, TB = 256, PER = TB / NT;
   __shared__ float tile[TB][CW + 1];
   __shared__ float tot[NT][CW];
   const int tid = threadIdx.x, col = tid % CW, g = tid / CW;
+  const bool summed = CW * (int)blockIdx.y + col < nsum;
   float* __restrict__ s = stats + (size_t)blockIdx.x * nb64 * sw + CW * blockIdx.y;
   float carry = 0.f;
   for (int t0 = 0; t0 < nb64; t0 += TB) {
@@ -191,9 +233,54 @@ __global__ __launch_bounds__(256) void stats_scan_kernel(float* __restrict__ sta
 #pragma unroll
     for (int i = 0; i < TB * CW / 256; ++i) {
       const int bl = g + NT * i;
-      if (bl < nt) s[(size_t)(t0 + bl) * sw + col] = tile[bl][col];
+      if (bl < nt && summed) s[(size_t)(t0 + bl) * sw + col] = tile[bl][col];
     }
     carry = all;
+    __syncthreads();
+  }
+  if (vt != nullptr && (int)blockIdx.y == (int)gridDim.y - 1)
+    vt_head_exponent(stats + (size_t)blockIdx.x * nb64 * sw + nsum, vt + (size_t)blockIdx.x * nb64 * vt_halves, nb64, sw,
+                     vt_halves);
+}
+
+// The head's V exponent E = max_b e_b over its blocks (e[b * sw] = e_b, written by the pack),
+// stored in every record (e[b * sw + 1]); blocks with e_b < E have their fp16 V^T multiplied by
+// 2^(e_b - E) in place.  Block exponents go through LDS 1024 at a time and each wave tests 64
+// of them with one ballot, so a head whose blocks share one exponent costs a few loads.
+__device__ void vt_head_exponent(float* __restrict__ e, uint16_t* __restrict__ vt, int nb64, int sw, int vt_halves) {
+  constexpr int TB = 1024;
+  __shared__ int ex[TB];
+  __shared__ int wmax[4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int m = -128;
+  for (int b = tid; b < nb64; b += 256) m = max(m, (int)e[(size_t)b * sw]);
+  m = (int)wave_max_u32((u32)(m + 1024)) - 1024;   // exponents are above -1024
+  if (lane == 0) wmax[w] = m;
+  __syncthreads();
+  const int E = max(max(wmax[0], wmax[1]), max(wmax[2], wmax[3]));
+  for (int t0 = 0; t0 < nb64; t0 += TB) {
+    const int nt = min(TB, nb64 - t0);
+    for (int i = tid; i < nt; i += 256) {
+      ex[i] = (int)e[(size_t)(t0 + i) * sw];
+      e[(size_t)(t0 + i) * sw + 1] = (float)E;
+    }
+    __syncthreads();
+    for (int c0 = 64 * w; c0 < nt; c0 += 256) {
+      const bool low = c0 + lane < nt && ex[c0 + lane] < E;
+      unsigned long long mask = __ballot(low);
+      while (mask != 0ull) {
+        const int i = __builtin_ctzll(mask);
+        mask &= mask - 1ull;
+        const float f = __builtin_ldexpf(1.0f, ex[c0 + i] - E);
+        u32x4* blk = reinterpret_cast<u32x4*>(vt + (size_t)(t0 + c0 + i) * vt_halves);
+        for (int u = lane; u < vt_halves / 8; u += 64) {
+          u32x4 x = blk[u];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x[j] = pack_f16x2(f16_lo_to_f32(x[j]) * f, f16_hi_to_f32(x[j]) * f);
+          blk[u] = x;
+        }
+      }
+    }
     __syncthreads();
   }
 }

@@ -11,8 +11,9 @@ constexpr int BN = 64;        // keys per LDS block
 constexpr int VROW = BN + 4;  // V^T row stride (bf16): 34 dwords -> conflict-free 8-byte reads
 
 // Global -> register -> LDS staging of one 64-key block of K (row-major) and V (transposed).
-// F16V converts V from bf16 to fp16 on the way (exact for 2^-14 <= |v| <= 65504; smaller
-// magnitudes keep an absolute error below 2^-25) so the P.V product can run as an fp16 MFMA.
+// F16V converts V from bf16 to fp16(v * vscale) on the way, vscale a power of two chosen by the
+// caller from max |v| so that the values land in fp16's normal range, so the P.V product can run
+// as an fp16 MFMA.
 template <int KS, int MT, bool VEC, bool F16V = false>
 struct BlockStager {
   static constexpr int DK = 16 * KS, DV = 32 * MT, KROW = DK + 8;
@@ -22,6 +23,7 @@ struct BlockStager {
   static constexpr int VPT = (VGROUPS + 255) / 256;
   u32x4 kr[KPT];
   u32x2 vr[VPT][4];
+  float vscale = 1.0f;   // F16V: V is stored as fp16(v * vscale), vscale a power of two
 
   __device__ __forceinline__ void load(const uint16_t* __restrict__ kg, const uint16_t* __restrict__ vg,
                                        int row0, int N, int d, int dv, int tid) {
@@ -89,10 +91,15 @@ struct BlockStager {
         const u32 b0 = vr[r][0][1], b1 = vr[r][1][1], b2 = vr[r][2][1], b3 = vr[r][3][1];
         u32x2 c0, c1, c2, c3;
         if (F16V) {
-          c0 = (u32x2){pack_f16x2(bf16_lo_to_f32(a0), bf16_lo_to_f32(a1)), pack_f16x2(bf16_lo_to_f32(a2), bf16_lo_to_f32(a3))};
-          c1 = (u32x2){pack_f16x2(bf16_hi_to_f32(a0), bf16_hi_to_f32(a1)), pack_f16x2(bf16_hi_to_f32(a2), bf16_hi_to_f32(a3))};
-          c2 = (u32x2){pack_f16x2(bf16_lo_to_f32(b0), bf16_lo_to_f32(b1)), pack_f16x2(bf16_lo_to_f32(b2), bf16_lo_to_f32(b3))};
-          c3 = (u32x2){pack_f16x2(bf16_hi_to_f32(b0), bf16_hi_to_f32(b1)), pack_f16x2(bf16_hi_to_f32(b2), bf16_hi_to_f32(b3))};
+          const float s = vscale;
+          c0 = (u32x2){pack_f16x2(bf16_lo_to_f32(a0) * s, bf16_lo_to_f32(a1) * s),
+                       pack_f16x2(bf16_lo_to_f32(a2) * s, bf16_lo_to_f32(a3) * s)};
+          c1 = (u32x2){pack_f16x2(bf16_hi_to_f32(a0) * s, bf16_hi_to_f32(a1) * s),
+                       pack_f16x2(bf16_hi_to_f32(a2) * s, bf16_hi_to_f32(a3) * s)};
+          c2 = (u32x2){pack_f16x2(bf16_lo_to_f32(b0) * s, bf16_lo_to_f32(b1) * s),
+                       pack_f16x2(bf16_lo_to_f32(b2) * s, bf16_lo_to_f32(b3) * s)};
+          c3 = (u32x2){pack_f16x2(bf16_hi_to_f32(b0) * s, bf16_hi_to_f32(b1) * s),
+                       pack_f16x2(bf16_hi_to_f32(b2) * s, bf16_hi_to_f32(b3) * s)};
         } else {
           c0 = (u32x2){(a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16)};
           c1 = (u32x2){(a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u)};
