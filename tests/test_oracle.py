@@ -161,10 +161,46 @@ def test_chunked_final_state_closed_form():
     assert torch.allclose(z[..., 0], torch.full_like(z[..., 0], 37.0))
 
 
-def test_identity_numerator_restatement():
-    q, k, v = _inputs(1, 1, 6, 4, 2, seed=12)
-    s = torch.tril(q @ k.transpose(-2, -1) / 2.0)
-    assert torch.allclose(ref.ref_identity_numerator(q, k, v), s @ v, rtol=1e-14)
+def _identity_loops(q, k, v):
+    """Causal identity-map numerator from the definition, scalar fp64 loops:
+    out[t] = sum_{u <= t} (q_t . k_u / sqrt(d)) v_u."""
+    qa, ka, va = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+    b, h, t, d = qa.shape
+    dv = va.shape[-1]
+    out = np.zeros((b, h, t, dv))
+    for bi in range(b):
+        for hi in range(h):
+            for ti in range(t):
+                for ui in range(ti + 1):
+                    s = sum(qa[bi, hi, ti, e] * ka[bi, hi, ui, e] for e in range(d)) / math.sqrt(d)
+                    for e in range(dv):
+                        out[bi, hi, ti, e] += s * va[bi, hi, ui, e]
+    return out
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 6, 4, 2), (2, 3, 9, 5, 3), (1, 2, 13, 16, 7)])
+def test_identity_numerator_brute_force(shape):
+    """ref_identity_numerator against scalar loops (odd d makes 1/sqrt(d) irrational; a
+    missing mask, a transposed product or the scale on both q and k fails this)."""
+    q, k, v = _inputs(*shape, seed=12)
+    got = ref.ref_identity_numerator(q, k, v).numpy()
+    want = _identity_loops(q, k, v)
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_identity_planted_mistakes_are_caught():
+    q, k, v = _inputs(1, 2, 9, 5, 3, seed=13)
+    want = _identity_loops(q, k, v)
+    d = q.shape[-1]
+    mask = torch.tril(torch.ones(9, 9, dtype=q.dtype))
+    wrong = [
+        (q / math.sqrt(d)) @ k.transpose(-2, -1) @ v,                                   # no causal mask
+        ((q / d) @ k.transpose(-2, -1) * mask) @ v,                                     # 1/d instead of 1/sqrt(d)
+        ((q / math.sqrt(d)) @ k.transpose(-2, -1) * torch.tril(mask, -1)) @ v,          # strict mask
+        (((q / math.sqrt(d)) @ k.transpose(-2, -1)).transpose(-2, -1) * mask) @ v,     # transposed scores
+    ]
+    for w in wrong:
+        assert not np.allclose(w.numpy(), want, rtol=1e-6, atol=1e-6)
 
 
 # ---------------------------------------------------------------- sliding window
