@@ -7,8 +7,9 @@ forward, so their state dicts load unchanged.
 Steps of a forward (hidden (b, t, dim) -> (b, t, dim)):
   * one GEMM for q, k and v over the three weights concatenated (rocBLAS / hipBLASLt through
     torch); the concatenation is cached and rebuilt when a weight is replaced or changed in place;
-  * its (b, t, 3, heads, head_dim) output viewed per head as (b, heads, t, head_dim) operands,
-    which the kernel wrappers make contiguous;
+  * its (b, t, 3, heads, head_dim) output permuted to (3, b, heads, t, head_dim) by one copy,
+    so that q, k and v are contiguous per-head operands (the kernels read each head's rows
+    contiguously; the wrappers then pass them on without copying);
   * the attention kernel: the fused parallel kernel (``solution_nki``, as the reference's NKI
     module) or ``solution`` (the chunked kernel from ``CHUNKED_MIN_T`` tokens);
   * the heads merged back to (b, t, dim), cast to the input dtype, and ``o_proj``.
@@ -82,7 +83,9 @@ class TrainiumBasedLinearAttentionNKI(nn.Module):
     def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
         b, t, _ = hidden_states.size()
         qkv = F.linear(hidden_states, self._qkv_weight()).view(b, t, 3, self.num_heads, self.head_dim)
-        q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+        # one permuting copy to (3, b, heads, t, head_dim): q, k and v are then contiguous
+        # slices, which the kernel wrappers take as they are (no copy per operand)
+        q, k, v = qkv.permute(2, 0, 3, 1, 4).contiguous().unbind(0)
         kernel = self._DISPATCH[self.dispatch]
         eps = self.eps
         y = _ForwardOnly.apply(lambda q_, k_, v_: kernel(q_, k_, v_, eps=eps), q, k, v)
