@@ -12,7 +12,8 @@ configuration (fp32 parallel, bf16 parallel, chunked, sliding, long-context chun
 headline workload (repeated to at least 10 s), on this host's cores.
 
 GPU time is measured with HIP events on the stream the kernels are launched on, around K
-back-to-back calls after W warm-up calls; HBM-bound configurations rotate through several
+back-to-back calls after W warm-up calls and at least --settle-ms (30) ms of back-to-back
+untimed calls, so that the card's clock has settled after the step from idle to load; HBM-bound configurations rotate through several
 input sets so that repeated calls do not run out of the 256 MB Infinity Cache.
 """
 
@@ -52,7 +53,10 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=5,
+                    help="untimed calls before each timed region (at least --settle-ms of calls run in any case)")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="minimum milliseconds of back-to-back untimed calls before each timed region")
     ap.add_argument("--rotate", type=int, default=4, help="input sets cycled through for HBM-bound configs")
     ap.add_argument("--configs", choices=["all", "none"], default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -175,12 +179,27 @@ class Call:
             self._check(rc, self.kind)
 
 
-def time_calls(calls, steps, warmup):
-    """Mean ms per call over ``steps`` back-to-back launches (HIP events on the launch stream)."""
+# Minimum duration of the warm-up before a timed region.  From idle, back-to-back calls of the
+# headline attention kernel run ~180 us, slow to ~215 us between the 10th and 20th call (the
+# card's clock controller reacting to the load step) and settle at ~185 us after ~10 ms; with
+# idle gaps every call takes ~181 us.  Timing starts once the clock has settled.
+SETTLE_MS = 30.0
+
+
+def time_calls(calls, steps, warmup, settle_ms=None):
+    """Mean ms per call over ``steps`` back-to-back launches (HIP events on the launch stream),
+    after at least ``warmup`` untimed calls and at least ``settle_ms`` of back-to-back work."""
     import torch
 
-    for i in range(warmup):
+    settle_ms = SETTLE_MS if settle_ms is None else settle_ms
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    i = 0
+    while i < warmup or (time.perf_counter() - t0) * 1e3 < settle_ms:
         calls[i % len(calls)]()
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()   # host time then tracks the GPU's
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -468,7 +487,9 @@ def load_traffic(kernel):
 
 
 def main():
+    global SETTLE_MS
     args = parse()
+    SETTLE_MS = args.settle_ms
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the multi-GPU sharding is described in "
               "DESIGN.md and not launched", file=sys.stderr)
@@ -538,6 +559,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": head["ms"],
         "higher_is_better": True,
         "scaling": "weak",

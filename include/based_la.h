@@ -64,7 +64,9 @@ const char* la_status_string(int status);
  * workspace: device scratch of at least la_based_parallel_workspace_bytes(...) bytes, 16-byte
  * aligned (may be NULL when that is 0).  It holds V repacked as fp16 V^T blocks and prefix
  * sums over 64-key blocks of the column sums of V, of k and of k k^T for the bf16, d = 16,
- * dv % 8 == 0, dv <= 64 kernel; its contents on return are unspecified.
+ * dv % 8 == 0, dv <= 64 kernel; for fp32 inputs on small grids (2 to 255 query blocks of 128
+ * tokens in all heads together) the partial numerators and row sums of every (query block,
+ * pair of 64-key blocks), which a second kernel adds; its contents on return are unspecified.
  * Limits: 1 <= d <= 128, 1 <= dv <= 128, scale > 0 and finite, eps >= 0 and finite.
  * The reference passes scale = 1/sqrt(d) and eps = 1e-6.
  */
@@ -80,8 +82,8 @@ int la_based_parallel_fwd(const void* q, const void* k, const void* v, int in_dt
  * and the attention kernel reading a workspace that already holds the pre-pass of the same k
  * and v (several calls with one k and v, or timing the attention kernel alone).  No counterpart in the
  * reference, whose parallel kernel has no pre-pass (kernels/nki_attention.py:33-115).  For
- * shapes with la_based_parallel_workspace_bytes(...) == 0 the pack is a no-op and
- * la_based_parallel_fwd_packed is la_based_parallel_fwd.  The packed kernels need q, k, out
+ * fp32 inputs and for shapes with la_based_parallel_workspace_bytes(...) == 0 the pack is a
+ * no-op and la_based_parallel_fwd_packed is la_based_parallel_fwd.  The packed kernels need q, k, out
  * 16-byte and v 8-byte aligned (LA_ERR_BAD_ALIGNMENT otherwise; la_based_parallel_fwd instead
  * falls back to its unpacked kernel).
  */

@@ -238,3 +238,32 @@ def test_packed_work_group_sizes(B, H, N, dv):
     want, _, want_den = ref.based_dense(q, k, v)
     assert err(y, want) < TOL_BF16
     assert err(den, want_den) < TOL_BF16
+
+
+@pytest.mark.parametrize("B,H,N,d,dv", [(1, 4, 1024, 16, 64), (1, 1, 300, 16, 100), (1, 2, 1000, 32, 128),
+                                        (2, 3, 257, 8, 24), (1, 1, 129, 4, 1)])
+def test_fp32_key_split(B, H, N, d, dv):
+    """fp32 inputs on small grids run every (query block, 64-key block) as its own work-group and
+    add the partial numerators and row sums in a second kernel: output, numerator and den against
+    fp64 (dv 100 and 128 the widest partials, dv 24 and 1 columns past dv in them; 300 and 257
+    tokens a ragged last query block, whose last key block may lie past N)."""
+    K = _kernels()
+    L = _lib_mod().lib()
+    need = L.la_based_parallel_workspace_bytes(B, H, N, d, dv, 0)
+    nqb = (N + 127) // 128
+    cols = 32 if dv <= 32 else (64 if dv <= 64 else 128)
+    assert need == B * H * nqb * (nqb + 1) * 128 * (cols + 1) * 4   # the split is in use
+    q, k, v = rand_qkv(B, H, N, d, dv, seed=N + dv, dtype=torch.float32, scale_qk=1.0 / math.sqrt(math.sqrt(d)))
+    want, want_num, want_den = ref.based_dense(q, k, v)
+    y, den = K.based_parallel(*to_dev(q, k, v), out_dtype=torch.float32, return_den=True)
+    num = K.based_parallel(*to_dev(q, k, v), normalize=False, out_dtype=torch.float32)
+    yb = K.based_parallel(*to_dev(q, k, v), out_dtype=torch.bfloat16)
+    e, en, ed = err(y, want), err(num, want_num), err(den, want_den)
+    print(f"B{B} H{H} N{N} d{d} dv{dv}: err={e:.2e} num={en:.2e} den={ed:.2e}")
+    assert e < TOL_F32 and en < TOL_F32 and ed < 1e-5
+    assert rounded_err(yb.float(), want) < 1e-2
+
+
+def _lib_mod():
+    from kernels import _lib
+    return _lib

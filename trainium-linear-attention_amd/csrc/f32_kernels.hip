@@ -13,6 +13,7 @@
 //           keys t-W+1..t, running max/sum per query.
 #include <float.h>
 
+#include "../../include/based_la.h"
 #include "la_common.hpp"
 #include "la_internal.hpp"
 
@@ -34,17 +35,37 @@ struct F32Params {
   void* out;
   float* den;
   const float* addend;   // sliding: optional fp32 addend of the output, or null
-  int BH, N, d, dv, nqb, window;
+  float* part;           // BASED key split: partial numerators [BH][nslot][BM][dv], then row sums
+                         // [BH][nslot][BM] (null: no split)
+  int BH, N, d, dv, nqb, window, nslot;
+  int vec;               // d % 4 == 0, dv % 4 == 0 and q, k, v 16-byte aligned: float4 loads
   float inv_c, inv_c2, fscale, eps, scale_log2;
   int normalize, out_f32;
 };
 
+// Key-split slot w of a head's nslot = nqb (nqb + 1): query block qb = the largest with
+// qb (qb + 1) <= w, then key block c = w - qb (qb + 1) (the float estimate is corrected exactly).
+__device__ __forceinline__ void split_slot(int wg, int nslot, int& bh, int& qb, int& c) {
+  bh = wg / nslot;
+  const int w = wg - bh * nslot;
+  int r = (int)((__builtin_sqrtf(4.0f * (float)w + 1.0f) - 1.0f) * 0.5f);
+  while ((r + 1) * (r + 2) <= w) ++r;
+  while (r * (r + 1) > w) --r;
+  qb = r;
+  c = w - r * (r + 1);
+}
+
 // SPLIT = 2 (BASED, small grids): two groups of four waves take the same 128 queries and every
 // other key block each, with a staging double buffer per group, and add their numerators and
 // row sums through LDS at the end, which halves the serial chain of key blocks of a query block.
-template <int KS, int MT, bool SLIDING, int SPLIT = 1>
+// PART (BASED, small grids): work-group (head, query block qb, c) takes key block c only
+// (c = 0 .. 2 qb + 1) and writes its unnormalised numerators and row sums to p.part; a combine
+// kernel adds the 2 qb + 2 partials of every query in a fixed order and normalises.  This spreads
+// a query block's keys over 2 qb + 2 compute units instead of one.
+template <int KS, int MT, bool SLIDING, int SPLIT = 1, bool PART = false>
 __global__ __launch_bounds__(256 * SPLIT) void f32_attn_kernel(const F32Params p) {
   static_assert(SPLIT == 1 || (SPLIT == 2 && !SLIDING), "key split: BASED only");
+  static_assert(!PART || (SPLIT == 1 && !SLIDING), "partial sums: BASED, one wave group");
   constexpr int DK = 16 * KS, DV = 32 * MT, BM = 128, HALF = DK / 2;
   constexpr int KROW = DK + 4;
   constexpr int KCH = BNF * DK / 4;              // float4 chunks in a K block
@@ -59,11 +80,15 @@ __global__ __launch_bounds__(256 * SPLIT) void f32_attn_kernel(const F32Params p
   const int grp = SPLIT == 2 ? __builtin_amdgcn_readfirstlane(tid_all >> 8) : 0;
   const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5, n = lane & 31;
   const int N = p.N, d = p.d, dv = p.dv, W = p.window;
-  int bh, qb;
-  map_causal_block(blockIdx.x, p.BH, p.nqb, bh, qb);
+  int bh, qb, pc = 0;
+  if (PART) {
+    split_slot(blockIdx.x, p.nslot, bh, qb, pc);
+  } else {
+    map_causal_block(blockIdx.x, p.BH, p.nqb, bh, qb);
+  }
   const int q0 = qb * BM;
-  const int jlo = SLIDING ? max(0, q0 - W + 1) / BNF : 0;
-  const int jhi = min((N - 1) / BNF, (q0 + BM - 1) / BNF);
+  const int jlo = PART ? pc : (SLIDING ? max(0, q0 - W + 1) / BNF : 0);
+  const int jhi = PART ? pc : min((N - 1) / BNF, (q0 + BM - 1) / BNF);
   const size_t hrow = (size_t)bh * N;
   const float* __restrict__ qg = p.q + hrow * d;
   const float* __restrict__ kg = p.k + hrow * d;
@@ -74,10 +99,21 @@ __global__ __launch_bounds__(256 * SPLIT) void f32_attn_kernel(const F32Params p
 
   // lane group h holds d-elements [HALF*h, HALF*h + HALF) of its query row
   float qf[HALF];
+  if (p.vec && HALF % 4 == 0) {
 #pragma unroll
-  for (int e = 0; e < HALF; ++e) {
-    const int col = HALF * h + e;
-    qf[e] = (query < N && col < d) ? qg[(size_t)query * d + col] : 0.f;
+    for (int e = 0; e < HALF; e += 4) {
+      const int col = HALF * h + e;
+      f32x4 x = {0.f, 0.f, 0.f, 0.f};
+      if (query < N && col < d) x = *reinterpret_cast<const f32x4*>(qg + (size_t)query * d + col);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qf[e + i] = x[i];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < HALF; ++e) {
+      const int col = HALF * h + e;
+      qf[e] = (query < N && col < d) ? qg[(size_t)query * d + col] : 0.f;
+    }
   }
 
   f32x16 acc[MT];
@@ -96,8 +132,12 @@ __global__ __launch_bounds__(256 * SPLIT) void f32_attn_kernel(const F32Params p
       const int row = row0 + key;
       f32x4 x = {0.f, 0.f, 0.f, 0.f};
       if (c < KCH && row < N) {
+        if (p.vec) {
+          if (col < d) x = *reinterpret_cast<const f32x4*>(kg + (size_t)row * d + col);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = (col + e < d) ? kg[(size_t)row * d + col + e] : 0.f;
+          for (int e = 0; e < 4; ++e) x[e] = (col + e < d) ? kg[(size_t)row * d + col + e] : 0.f;
+        }
       }
       kr[r] = x;
     }
@@ -110,8 +150,12 @@ __global__ __launch_bounds__(256 * SPLIT) void f32_attn_kernel(const F32Params p
         const int row = row0 + 4 * kg4 + i;
         f32x4 x = {0.f, 0.f, 0.f, 0.f};
         if (g < VGR && row < N) {
+          if (p.vec) {
+            if (4 * g4 < dv) x = *reinterpret_cast<const f32x4*>(vg + (size_t)row * dv + 4 * g4);
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) x[e] = (4 * g4 + e < dv) ? vg[(size_t)row * dv + 4 * g4 + e] : 0.f;
+            for (int e = 0; e < 4; ++e) x[e] = (4 * g4 + e < dv) ? vg[(size_t)row * dv + 4 * g4 + e] : 0.f;
+          }
         }
         vr[r][i] = x;
       }
@@ -237,6 +281,20 @@ __global__ __launch_bounds__(256 * SPLIT) void f32_attn_kernel(const F32Params p
 
   if (!wave_live) return;
   const float rs = rsum + __shfl_xor(rsum, 32);
+  if (PART) {
+    // slot (bh, qb, pc) in the accumulator order [wave][mt][lane][16] (DV = 32 MT columns), so
+    // that every lane stores whole 16-byte pieces and the wave one contiguous run per mt
+    const size_t slot = (size_t)bh * p.nslot + (size_t)qb * (qb + 1) + pc;
+    float* num = p.part + (slot * 4 + w) * (size_t)(MT * 1024) + 16 * lane;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4*>(num + mt * 1024 + 4 * g) =
+            (f32x4){acc[mt][4 * g], acc[mt][4 * g + 1], acc[mt][4 * g + 2], acc[mt][4 * g + 3]};
+    if (h == 0) p.part[(size_t)p.BH * p.nslot * 128 * (MT * 32) + slot * BM + 32 * w + n] = rs;
+    return;
+  }
   if (query >= N) return;
   float inv;
   if (SLIDING) {
@@ -262,10 +320,70 @@ __global__ __launch_bounds__(256 * SPLIT) void f32_attn_kernel(const F32Params p
     }
 }
 
+// Combine of the key-split partials of query block qb: slots c = 0 .. 2 qb + 1 added in that
+// order and normalised.  The numerators are in the split kernel's accumulator order
+// [wave][mt][lane][16]: thread -> one 16-byte piece (wave w, mt, lane (n, h), group g), i.e. query
+// 32 w + n, columns 32 mt + 8 g + 4 h .. +3, read coalesced from every slot; a batch of eight
+// slots is loaded before any is added (a dependent load per slot would serialise on the L2
+// latency).  Work-group (head, query block, 256 pieces).
+template <int MT>
+__global__ __launch_bounds__(256) void f32_split_combine_kernel(const F32Params p) {
+  constexpr int BM = 128, PIECES = 4 * MT * 64 * 4, WPB = PIECES / 256;
+  const int tid = threadIdx.x, bh = blockIdx.y, qb = blockIdx.x / WPB;
+  const int pc = (blockIdx.x - qb * WPB) * 256 + tid;    // piece
+  const int w = pc / (MT * 256), mt = (pc / 256) % MT, lane = (pc / 4) % 64, g = pc % 4;
+  const int n = lane & 31, h = lane >> 5;
+  const int N = p.N, dv = p.dv, q0 = qb * BM, row = q0 + 32 * w + n, col = 32 * mt + 8 * g + 4 * h;
+  if (row >= N) return;
+  const int ns = 2 * qb + 2;
+  const size_t slot0 = (size_t)bh * p.nslot + (size_t)qb * (qb + 1);
+  const float* dens = p.part + (size_t)p.BH * p.nslot * BM * (MT * 32);
+  const float* base = p.part + slot0 * (size_t)(BM * MT * 32) + (size_t)w * (MT * 1024) + mt * 1024 + 16 * lane + 4 * g;
+  float den = 0.f;
+  f32x4 x = {0.f, 0.f, 0.f, 0.f};
+  for (int b0 = 0; b0 < ns; b0 += 8) {
+    float t[8];
+    f32x4 u[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const bool ok = b0 + c < ns;
+      t[c] = ok ? dens[(slot0 + b0 + c) * BM + 32 * w + n] : 0.f;
+      u[c] = ok ? *reinterpret_cast<const f32x4*>(base + (size_t)(b0 + c) * (BM * MT * 32)) : (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      den += t[c];
+      x += u[c];
+    }
+  }
+  const size_t hrow = (size_t)bh * N;
+  if (p.den != nullptr && col == 0) p.den[hrow + row] = den;
+  const float inv = p.normalize ? 1.0f / (den + p.eps) : 1.0f;
+  const size_t o = (hrow + row) * (size_t)dv + col;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (col + e >= dv) break;
+    if (p.out_f32)
+      static_cast<float*>(p.out)[o + e] = x[e] * inv;
+    else
+      static_cast<uint16_t*>(p.out)[o + e] = f32_to_bf16_bits(x[e] * inv);
+  }
+}
+
 template <int KS, int MT, bool SL>
 int launch_f32(F32Params p, hipStream_t stream) {
   p.nqb = (p.N + 127) / 128;
   const dim3 grid((unsigned)(p.nqb * p.BH));
+  if constexpr (!SL) {
+    if (p.part != nullptr) {
+      // key split over work-groups (the workspace was sized for it: f32_split_slots)
+      hipLaunchKernelGGL((f32_attn_kernel<KS, MT, SL, 1, true>), dim3((unsigned)(p.BH * p.nslot)), dim3(256), 0,
+                         stream, p);
+      hipLaunchKernelGGL(f32_split_combine_kernel<MT>, dim3((unsigned)(p.nqb * 4 * MT), (unsigned)p.BH), dim3(256), 0,
+                         stream, p);
+      return (int)hipGetLastError();
+    }
+  }
   if constexpr (!SL && KS == 1 && MT <= 2) {
     // fewer query blocks than CUs: split every query block's keys over two wave groups
     if ((long long)p.nqb * p.BH < device_cu_count()) {
@@ -294,6 +412,23 @@ int dispatch_f32(const F32Params& p, hipStream_t stream) {
 
 }  // namespace
 
+// Key split of the fp32 BASED kernel: for grids of fewer 128-query blocks than 256 (a quarter of
+// MI355X's work-group slots) with at least two query blocks, every (query block, 64-key block)
+// runs as its own work-group.  Slots per head (2 qb + 2 for query block qb), or 0 when the split
+// is not used (also when its partials would pass 2048 slots in all).
+int f32_split_slots(int BH, int N) {
+  const long long nqb = (N + 127) / 128;
+  if (nqb < 2 || nqb * BH >= 256) return 0;
+  const long long ns = nqb * (nqb + 1);
+  return ns * BH <= 2048 ? (int)ns : 0;
+}
+
+size_t f32_split_workspace_bytes(int BH, int N, int dv) {
+  const int ns = f32_split_slots(BH, N);
+  const size_t cols = dv <= 32 ? 32 : (dv <= 64 ? 64 : 128);   // the kernel's 32 MT columns
+  return ns == 0 ? 0 : (size_t)BH * ns * 128 * (cols + 1) * sizeof(float);
+}
+
 int launch_based_parallel_fp32(const ParallelArgs& a, hipStream_t stream) {
   F32Params p{};
   p.q = static_cast<const float*>(a.q);
@@ -312,6 +447,14 @@ int launch_based_parallel_fp32(const ParallelArgs& a, hipStream_t stream) {
   p.eps = a.eps;
   p.normalize = a.normalize ? 1 : 0;
   p.out_f32 = a.out_f32 ? 1 : 0;
+  p.vec = (a.d % 4 == 0) && (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+          ((reinterpret_cast<uintptr_t>(a.k) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 15) == 0);
+  p.nslot = f32_split_slots(a.BH, a.N);
+  if (p.nslot > 0) {
+    if (a.workspace == nullptr || a.workspace_bytes < f32_split_workspace_bytes(a.BH, a.N, a.dv))
+      return LA_ERR_WORKSPACE;
+    p.part = static_cast<float*>(a.workspace);
+  }
   return dispatch_f32<false>(p, stream);
 }
 
@@ -329,6 +472,8 @@ int launch_sliding_window_f32(const SlidingArgs& a, hipStream_t stream) {
   p.window = a.window;
   p.scale_log2 = (float)((double)a.scale * 1.4426950408889634);
   p.out_f32 = a.out_f32 ? 1 : 0;
+  p.vec = (a.d % 4 == 0) && (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
+          ((reinterpret_cast<uintptr_t>(a.k) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 15) == 0);
   return dispatch_f32<true>(p, stream);
 }
 

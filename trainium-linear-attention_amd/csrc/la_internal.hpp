@@ -86,6 +86,8 @@ struct FeatureMapArgs {
 // and returns 0, a negative LA_ERR_* code, or a positive hipError_t.
 int launch_based_parallel(const ParallelArgs& a, hipStream_t stream);
 size_t parallel_workspace_bytes(int BH, int N, int d, int dv, bool in_f32);
+int f32_split_slots(int BH, int N);                         // fp32 key split: slots per head, or 0
+size_t f32_split_workspace_bytes(int BH, int N, int dv);    // its partials (0 without the split)
 bool parallel_packed_shape(int d, int dv, bool in_f32);   // shapes of the packed (pre-pass) kernel
 int launch_sliding_window(const SlidingArgs& a, hipStream_t stream);
 size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk);
