@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 7
+#define LA_ABI_VERSION 8
 
 /* element types */
 #define LA_F32 0
@@ -181,6 +181,23 @@ int la_sliding_window_fwd(const void* q, const void* k, const void* v, int in_dt
 int la_sliding_window_fwd_add(const void* q, const void* k, const void* v, int in_dtype,
                               const float* addend, void* out, int out_dtype, int B, int H, int N,
                               int d, int dv, int window, float scale, void* hip_stream);
+
+/*
+ * The full BASED layer in one output launch: out = linear_attention(q, k, v) +
+ * sliding_window_softmax(q_sw, k_sw, v) (kernels/nki_attention_sliding.py:4-5, whose two
+ * branches the reference computes in separate calls; no single reference entry point).  The
+ * linear branch is la_based_chunked_fwd's (scale, eps, normalised), the softmax branch
+ * la_sliding_window_fwd's (scale_sw, window); after the chunked state passes one kernel computes
+ * both branches per (head, segment) and stores their sum, rounded once to out_dtype.
+ * q, k: (B,H,N,16); q_sw, k_sw: (B,H,N,d_sw); v, out: (B,H,N,dv); all bf16 inputs, every
+ * tensor 16-byte aligned.  workspace: la_based_chunked_workspace_bytes(B, H, N, 16, dv, 64)
+ * bytes, 16-byte aligned.  Limits: d = 16, dv % 8 == 0 and dv <= 64, d_sw in {16, 32, 64},
+ * 1 <= window <= 64 (LA_ERR_UNSUPPORTED_DIM otherwise; such layers are the two calls).
+ */
+int la_based_layer_fwd(const void* q, const void* k, const void* v, const void* q_sw, const void* k_sw,
+                       int in_dtype, void* out, int out_dtype, int B, int H, int N, int d, int dv, int d_sw,
+                       int window, float scale, float scale_sw, float eps, void* workspace,
+                       size_t workspace_bytes, void* hip_stream);
 
 /*
  * One decode step of BASED attention on an exported state (no reference counterpart: the

@@ -28,7 +28,7 @@ def test_header_declares_expected_entry_points():
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
         "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_chunk_used", "la_based_chunked_fwd",
         "la_based_chunked_fwd_continue", "la_based_chunked_fwd_noalloc", "la_sliding_window_fwd",
-        "la_sliding_window_fwd_add", "la_based_decode_step", "la_based_decode_workspace_bytes",
+        "la_sliding_window_fwd_add", "la_based_layer_fwd", "la_based_decode_step", "la_based_decode_workspace_bytes",
         "la_based_decode_step_ws", "la_identity_workspace_bytes", "la_identity_linear_fwd",
         "la_taylor_feature_map"])
 
@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib()
-    assert lib.la_abi_version() == 7
+    assert lib.la_abi_version() == 8
     for code in range(-10, 1):
         s = lib.la_status_string(code).decode()
         assert s and s != "unknown status"
@@ -106,6 +106,34 @@ def test_sliding_add_argument_errors():
     assert call(12, 0) == -4                       # window
     assert call(10, 129) == -5                     # d
     assert call(9, 0) == 0                         # N = 0: nothing to launch
+
+
+def test_layer_argument_errors():
+    """la_based_layer_fwd rejects what its kernel does not take before anything is launched."""
+    lib = _lib()
+    f = lib.la_based_layer_fwd
+    need = lib.la_based_chunked_workspace_bytes(1, 1, 8, 16, 64, 64)
+    W = ctypes.c_void_p(1 << 24)
+    # q, k, v, q_sw, k_sw, dtype, out, out_dtype, B, H, N, d, dv, d_sw, window, scale, scale_sw, eps, ws, bytes, stream
+    ok = [P, P, P, P, P, 1, P, 1, 1, 1, 8, 16, 64, 64, 64, 0.25, 0.125, 1e-6, W, need, None]
+
+    def call(i, x):
+        a = list(ok)
+        a[i] = x
+        return f(*a)
+
+    assert call(3, None) == -1                     # q_sw
+    assert call(4, None) == -1                     # k_sw
+    assert call(5, 0) == -3                        # fp32 inputs: the two-launch layer
+    assert call(11, 32) == -5                      # d != 16
+    assert call(12, 72) == -5                      # dv > 64
+    assert call(12, 20) == -5                      # dv % 8 != 0
+    assert call(13, 48) == -5                      # d_sw not 16, 32 or 64
+    assert call(14, 65) == -5                      # window > 64
+    assert call(14, 0) == -5                       # window < 1
+    assert call(16, 0.0) == -4                     # scale_sw
+    assert call(3, ctypes.c_void_p((1 << 20) + 8)) == -8   # q_sw not 16-byte aligned
+    assert call(10, 0) == 0                        # N = 0: nothing to launch
 
 
 def test_chunked_continue_argument_errors():

@@ -44,6 +44,7 @@
 //     computes every segment's state increment (fp16 S^T, fp32 G) into the workspace, kernel 2
 //     turns them into exclusive prefixes, kernel 3 runs the chunk recurrence of all segments
 //     in parallel from those prefixes.
+#include <float.h>
 #include <math.h>
 
 #include "../../include/based_la.h"
@@ -161,6 +162,12 @@ struct ChunkParams {
   const float* state_in;             // optional initial state, reference basis (BH, 153, dv + 1)
   float prev_tokens;                 // tokens summarised by state_in (0 without one)
   int normalize, out_f32, vec_out;
+  // full layer (chunked_layer_kernel): the sliding-window softmax branch's q_sw, k_sw (BH, N, dsw)
+  // bf16, its window and scale * log2(e)
+  const uint16_t* qsw;
+  const uint16_t* ksw;
+  int window;
+  float sw_log2;
 };
 
 __device__ __forceinline__ void map_segment(int wg, int BH, int P, int& bh, int& p) {
@@ -190,6 +197,32 @@ struct OutLds {
   u32 xk[2][NWAVE_OUT];         // max |k| (bf16 bits) of the next chunk
   int eg;                       // exponent of G16
 };
+// LDS image of the full-layer kernel: the chunk recurrence's tables with V^T in a ring of two
+// chunks (slot = absolute chunk index & 1: the softmax branch reads the previous chunk's keys),
+// the softmax branch's K_sw rows in a ring of two chunks, the chunk's linear-branch outputs
+// (normalised, fp32) handed from the recurrence waves to the softmax waves, and the exponent of
+// each V^T slot.
+constexpr int YLS = 68;         // row stride (floats) of the handed-over linear outputs
+template <int DSW>
+struct LayerLds {
+  uint16_t Q0[CH * QRS];
+  uint16_t Kr[CH * QRS];
+  uint16_t KT[KT_ROWS * KRS];
+  uint16_t VT2[2][64 * KRS];
+  uint16_t ST[64 * STS];
+  uint16_t G16[32 * GRS];
+  u32 xs[2][NWAVE_OUT];
+  u32 xv[2][NWAVE_OUT];
+  u32 xk[2][NWAVE_OUT];
+  int eg;
+  int Us[2];
+  uint16_t KSW[2][CH * (DSW + 8)];
+  float YL[CH * YLS];
+};
+__device__ __forceinline__ uint16_t* vtab(OutLds& L, int) { return L.VT; }
+template <int DSW>
+__device__ __forceinline__ uint16_t* vtab(LayerLds<DSW>& L, int slot) { return L.VT2[slot]; }
+
 struct SegTables {
   uint16_t KT[KT_ROWS * KRS];
   uint16_t VT[64 * KRS];
@@ -815,8 +848,8 @@ struct OwnedBlocks {
 };
 constexpr int kGramWave = 1;
 
-template <int NB>
-__device__ __forceinline__ void publish_state(OutLds& L, const f32x16 (&S)[NB][2], int first, int r, int h) {
+template <int NB, class LT>
+__device__ __forceinline__ void publish_state(LT& L, const f32x16 (&S)[NB][2], int first, int r, int h) {
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     const int blk = first + b;
@@ -836,7 +869,8 @@ __device__ __forceinline__ void publish_state(OutLds& L, const f32x16 (&S)[NB][2
 // fp16 Gram matrix for the denominator, with the token count G(16,16) left out (it is added
 // exactly), in units of 2^eg with eg from its largest entry (entries below 2^14).  Lane (col
 // j = r, rows 8 jj + 4 h + i) writes row j by symmetry.
-__device__ __forceinline__ void publish_gram(OutLds& L, const f32x16& G, int r, int h) {
+template <class LT>
+__device__ __forceinline__ void publish_gram(LT& L, const f32x16& G, int r, int h) {
   float g[16];
   float m = 0.f;
 #pragma unroll
@@ -854,6 +888,174 @@ __device__ __forceinline__ void publish_gram(OutLds& L, const f32x16& G, int r, 
   if (r == 0 && h == 0) L.eg = eg;
 }
 
+// Softmax branch of the full layer for one wave: queries 32W .. 32W + 31 of every chunk of the
+// segment, keys t - window + 1 .. t (window <= 64), scores on bf16 MFMAs over DSW dims, online
+// softmax in fp32 (exp2 of log2-scaled scores), P in fp16 against the recurrence's fp16 V^T
+// (units 2^U), the outputs added to the recurrence's handed-over ones and stored
+// (benchmarks/sliding_attention_benchmark.py:32-56 for the branch, kernels/nki_attention_sliding.py:4-5
+// for the sum).  K_sw rows of the chunk are staged by the four softmax waves, a 32-row quarter each;
+// those of the 64 tokens before the segment, and their V, in the prologue.
+template <int DSW>
+struct SwRole {
+  static constexpr int KS = DSW > 0 ? DSW / 16 : 1;   // K-steps of a score tile; 16-byte pieces per lane
+  static constexpr int KSS = DSW + 8;                  // K_sw row stride (halves)
+  u32x4 qf[KS];          // Q_sw of the chunk's queries: lane (query r, half h) holds dims 16 kk + 8 h ..
+  u32x4 kst[KS];         // the next chunk's K_sw quarter, in flight
+  f32x16 O[2];           // numerator of the branch, V^T units of the chunk
+  float ysc;             // 2^U / (softmax row sum)
+  __amdgpu_buffer_rsrc_t rq, rk;
+  size_t hrow;
+
+  __device__ __forceinline__ void init(const ChunkParams& p, int bh, int, int) {
+    hrow = (size_t)bh * p.N;
+    rq = make_rsrc(p.qsw + hrow * DSW, (u32)p.N * (u32)(DSW * 2));
+    rk = make_rsrc(p.ksw + hrow * DSW, (u32)p.N * (u32)(DSW * 2));
+  }
+  __device__ __forceinline__ void load_k(int cabs, int W, int lane) {
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      const int pc = lane + 64 * i, row = pc / (DSW / 8), c8 = pc % (DSW / 8);
+      kst[i] = buf_load_b128(rk, ((cabs * CH + 32 * W + row) * DSW + 8 * c8) * 2);
+    }
+  }
+  template <class LT>
+  __device__ __forceinline__ void store_k(LT& L, int cabs, int W, int lane) {
+#pragma unroll
+    for (int i = 0; i < KS; ++i) {
+      const int pc = lane + 64 * i, row = pc / (DSW / 8), c8 = pc % (DSW / 8);
+      *reinterpret_cast<u32x4*>(&L.KSW[cabs & 1][(32 * W + row) * KSS + 8 * c8]) = kst[i];
+    }
+  }
+  __device__ __forceinline__ void load_q(int cabs, int W, int lane) {
+    const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) qf[kk] = buf_load_b128(rq, ((cabs * CH + 32 * W + r) * DSW + 16 * kk + 8 * h) * 2);
+  }
+  // V of this wave's 16 of the 64 tokens before chunk c0 (zero before the sequence) into columns
+  // 64 + 16 W .. of the previous chunk's V^T slot, as fp16(v 2^-U); lane = V^T row (dv column)
+  template <class LT>
+  __device__ __forceinline__ void prev_v(LT& L, const ChunkParams& p, int c0, int U, int W, int lane) {
+    const uint16_t* vh = p.v + hrow * p.dv;
+    const float vs = __builtin_ldexpf(1.0f, -U);
+    uint16_t* vt = vtab(L, (c0 + 1) & 1);
+#pragma unroll
+    for (int tp = 0; tp < 8; ++tp) {
+      const int col = 64 + 16 * W + 2 * tp;          // chunk-local column of the previous chunk
+      const int t = c0 * CH - CH + col;               // its token
+      float a = 0.f, b = 0.f;
+      if (lane < p.dv && t >= 0) {
+        a = bf16_lo_to_f32(vh[(size_t)t * p.dv + lane]) * vs;
+        b = bf16_lo_to_f32(vh[(size_t)(t + 1) * p.dv + lane]) * vs;
+      }
+      *reinterpret_cast<u32*>(&vt[vt_off(lane, col >> 3) + (col & 7)]) = pack_f16x2(a, b);
+    }
+    if (W == 0 && lane == 0) L.Us[(c0 + 1) & 1] = U;
+  }
+  template <class LT>
+  __device__ __forceinline__ void prologue(LT& L, const ChunkParams& p, int c0, int U, int W, int lane) {
+    load_k(c0, W, lane);
+    load_q(c0, W, lane);
+    // K_sw rows of this wave's 16 of the 64 tokens before chunk c0
+    for (int pc = lane; pc < 16 * (DSW / 8); pc += 64) {
+      const int row = pc / (DSW / 8), c8 = pc % (DSW / 8);
+      const int t = c0 * CH - 64 + 16 * W + row;
+      const u32x4 x = buf_load_b128(rk, t >= 0 ? (t * DSW + 8 * c8) * 2 : kOffOutOfRange);
+      *reinterpret_cast<u32x4*>(&L.KSW[(c0 + 1) & 1][(64 + 16 * W + row) * KSS + 8 * c8]) = x;
+    }
+    prev_v(L, p, c0, U, W, lane);
+    store_k(L, c0, W, lane);
+  }
+  template <class LT>
+  __device__ __forceinline__ void phase1(LT& L, const ChunkParams& p, int cabs, int W, int lane, bool more) {
+    if (more) load_k(cabs + 1, W, lane);
+    const int r = lane & 31, h = lane >> 5, qs = 32 * W, q = qs + r;
+    const int Uc = __builtin_amdgcn_readfirstlane(L.Us[cabs & 1]);
+    const int Upv = __builtin_amdgcn_readfirstlane(L.Us[(cabs + 1) & 1]);
+    O[0] = splat16(0.f);
+    O[1] = splat16(0.f);
+    float mrun = -FLT_MAX, lrun = 0.f;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int kb = qs - 64 + 32 * j;                       // chunk-local first key of the tile
+      if (kb + 31 < qs - p.window + 1 || cabs * CH + kb + 31 < 0) continue;   // outside every window
+      const bool prev = kb < 0;
+      const int slot = prev ? (cabs + 1) & 1 : cabs & 1;
+      const int kc = prev ? kb + CH : kb;
+      // S^T = K_sw Q_sw^T with the key rows in perm32 order: the accumulator is the P.V operand
+      f32x16 sc = splat16(0.f);
+      const uint16_t* krow = &L.KSW[slot][(kc + perm32(r)) * KSS + 8 * h];
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) sc = mfma32x32x16(*reinterpret_cast<const u32x4*>(krow + 16 * kk), qf[kk], sc);
+      // element e of lane (query r, half h) is key kb + 16 (e >> 3) + 8 h + (e & 7)
+      float x[16];
+      float mt = -FLT_MAX;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = kb + 16 * (e >> 3) + 8 * h + (e & 7);
+        const bool ok = key <= q && key > q - p.window && cabs * CH + key >= 0;
+        x[e] = ok ? sc[e] * p.sw_log2 : -FLT_MAX;
+        mt = __builtin_fmaxf(mt, x[e]);
+      }
+      mt = __builtin_fmaxf(mt, __shfl_xor(mt, 32));   // both halves of the query's row
+      const float mnew = __builtin_fmaxf(mrun, mt);
+      const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+      lrun *= alpha;
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) O[n][e] *= alpha;
+      mrun = mnew;
+      // previous chunk's V^T in its own units: P scaled by 2^(U_prev - U) (1 unless U rose)
+      const float pf = prev ? __builtin_ldexpf(1.0f, Upv - Uc) : 1.0f;
+      u32 pk[8];
+#pragma unroll
+      for (int xx = 0; xx < 8; ++xx) {
+        const float p0 = x[2 * xx] == -FLT_MAX ? 0.f : __builtin_amdgcn_exp2f(x[2 * xx] - mnew);
+        const float p1 = x[2 * xx + 1] == -FLT_MAX ? 0.f : __builtin_amdgcn_exp2f(x[2 * xx + 1] - mnew);
+        lrun += p0 + p1;
+        pk[xx] = pack_f16x2(p0 * pf, p1 * pf);
+      }
+      const uint16_t* vt = vtab(L, slot);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const u32x4 bp = {pk[4 * s], pk[4 * s + 1], pk[4 * s + 2], pk[4 * s + 3]};
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+          O[n] = mfma32x32x16_f16(*reinterpret_cast<const u32x4*>(&vt[vt_off(32 * n + r, kc / 8 + 2 * s + h)]), bp, O[n]);
+      }
+    }
+    const float l = lrun + __shfl_xor(lrun, 32);   // > 0: each query's own key is in its window
+    ysc = __builtin_ldexpf(1.0f, Uc) / l;
+  }
+  template <bool OUT_F32, class LT>
+  __device__ __forceinline__ void phase2(LT& L, const ChunkParams& p, int cabs, int W, int lane, bool more) {
+    constexpr int esz = OUT_F32 ? 4 : 2;
+    const int r = lane & 31, h = lane >> 5, qs = 32 * W, row0 = cabs * CH, dv = p.dv;
+    const __amdgpu_buffer_rsrc_t ro =
+        make_rsrc(static_cast<char*>(p.out) + (hrow + row0) * dv * esz, (u32)(p.N - row0) * (u32)dv * (u32)esz);
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int col = 32 * n + 8 * jj + 4 * h;
+        const f32x4 yl = *reinterpret_cast<const f32x4*>(&L.YL[(qs + r) * YLS + col]);
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = yl[e] + O[n][4 * jj + e] * ysc;
+        const int voff = col < dv ? ((qs + r) * dv + col) * esz : kOffOutOfRange;
+        if (OUT_F32)
+          buf_store_b128(__builtin_bit_cast(u32x4, (f32x4){y[0], y[1], y[2], y[3]}), ro, voff);
+        else
+          buf_store_b64((u32x2){pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])}, ro, voff);
+      }
+    }
+    if (more) {
+      store_k(L, cabs + 1, W, lane);
+      load_q(cabs + 1, W, lane);
+    }
+  }
+};
+
 // VEC: v rows 16-byte aligned with dv % 8 == 0 and out 16-byte aligned with dv % 4 == 0 (buffer
 // loads and stores); otherwise element-wise accesses with bounds checks.
 //
@@ -861,8 +1063,19 @@ __device__ __forceinline__ void publish_gram(OutLds& L, const f32x16& G, int r, 
 // the 1/4), the published S^T is fp16(S), V^T is fp16(v 2^-U), the intra-chunk P is fp16(p / 2),
 // so O = S^T phi(Q)^T + V^T P^T is num / 2 in units of 2^U.  The Gram registers G hold
 // (sum g g^T) / 4 and the published copy G16 is fp16(G 2^-EG).
-template <int W, bool VEC, bool OUT_F32>
-__device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int bh, int seg) {
+//
+// Full layer (LT = LayerLds<DSW>, DSW > 0): the work-group has 8 waves.  ROLE 0..3 run the chunk
+// recurrence as above but hand their normalised outputs to LDS; ROLE 4..7 compute the
+// sliding-window softmax of the same 32 queries (window <= 64: key tiles 64 and 32 tokens before
+// the queries and their own, from the V^T ring and the K_sw ring), add the handed-over linear
+// outputs and store.  Every barrier sits in code both roles run, with uniform conditions, so the
+// roles pass the same barriers.
+template <int ROLE, bool VEC, bool OUT_F32, class LT = OutLds, int DSW = 0>
+__device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh, int seg) {
+  constexpr bool LAYER = DSW > 0;
+  constexpr bool LIN = ROLE < NWAVE_OUT;   // recurrence role (the only one without LAYER)
+  constexpr int W = LIN ? ROLE : ROLE - NWAVE_OUT;
+  static_assert(!LAYER || VEC, "the layer kernel takes the vector path");
   using OB = OwnedBlocks<W>;
   constexpr int NB = OB::NB;
   constexpr bool GRAM = W == kGramWave;
@@ -907,7 +1120,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
   int U = kNoExp;   // exponent of the state registers and of V^T (the same in every wave)
   StageRegs st;
   StageConv cv;
-  stage_load<VEC, true>(st, p, qh, kh, vh, c0 * CH, lane, W);
+  if constexpr (LIN) stage_load<VEC, true>(st, p, qh, kh, vh, c0 * CH, lane, W);
   if (seg > 0 || p.state_in != nullptr) {
     // prefix of the earlier segments (with the caller's initial state, when there is one); the
     // first segment's is slot P - 1, which holds the initial state alone
@@ -915,7 +1128,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
     U = seg > 0 ? p.wsEP[slot] : p.wsE[slot];
     const uint16_t* ws = p.wsS + slot * (64 * NF);
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
+    for (int b = 0; b < (LIN ? NB : 0); ++b) {
       const int blk = OB::first + b;
 #pragma unroll
       for (int n = 0; n < 2; ++n) {
@@ -930,7 +1143,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
         }
       }
     }
-    if (GRAM) {
+    if (GRAM && LIN) {
       const float* gin = p.wsG + slot * 1024 + lane * 16;
 #pragma unroll
       for (int e = 0; e < 16; e += 4) {
@@ -949,22 +1162,32 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
   // written again behind one more barrier (the same decision in every wave).
   const int Up = U;   // kNoExp without a prefix
   U = max(Up, 0);
-  if (Up != kNoExp && U != Up) acc_scale<NB>(S, __builtin_ldexpf(1.0f, Up - U));
-  init_kt_constants(L.KT, tid, 64 * NWAVE_OUT);
-  publish_state<NB>(L, S, OB::first, r, h);
-  if (GRAM) publish_gram(L, G, r, h);
-  stage_convert_qk<true>(st, cv, p.qs, p.ks, lane);
-  if (U == 0)
-    stage_convert_v(st, cv);
-  else
-    stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -U));
-  stage_write<true>(cv, L.Q0, L.Kr, L.KT, L.VT, lane, W);
-  {
-    const u32 mvk = wave_max_u16x2((stage_vmax(st) << 16) | stage_kmax(st));
-    if (lane == 0) {
-      L.xv[0][W] = mvk >> 16;
-      L.xk[0][W] = mvk & 0xffffu;
+  // softmax role: its slice of the sliding-window branch (queries 32W .. 32W + 31 of each chunk)
+  SwRole<DSW> sw;
+  if constexpr (LIN) {
+    if (Up != kNoExp && U != Up) acc_scale<NB>(S, __builtin_ldexpf(1.0f, Up - U));
+    init_kt_constants(L.KT, tid, 64 * NWAVE_OUT);
+    publish_state<NB>(L, S, OB::first, r, h);
+    if (GRAM) publish_gram(L, G, r, h);
+    stage_convert_qk<true>(st, cv, p.qs, p.ks, lane);
+    if (U == 0)
+      stage_convert_v(st, cv);
+    else
+      stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -U));
+    stage_write<true>(cv, L.Q0, L.Kr, L.KT, vtab(L, c0 & 1), lane, W);
+    {
+      const u32 mvk = wave_max_u16x2((stage_vmax(st) << 16) | stage_kmax(st));
+      if (lane == 0) {
+        L.xv[0][W] = mvk >> 16;
+        L.xk[0][W] = mvk & 0xffffu;
+      }
     }
+    if constexpr (LAYER) {
+      if (W == 0 && lane == 0) L.Us[c0 & 1] = U;
+    }
+  } else {
+    sw.init(p, bh, W, lane);
+    sw.prologue(L, p, c0, U, W, lane);
   }
   lds_barrier();
   // the current chunk's max |v| and |k| exponents, for the bound on its state increment
@@ -972,12 +1195,19 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
   int eKc = exp_of_f32bits(lds_max4(L.xk[0]) << 16);
   {
     const int U0 = max(Up, first_unit(eVc));
-    if (U0 != U) {   // rare, and the same in every wave
-      acc_scale<NB>(S, __builtin_ldexpf(1.0f, U - U0));
+    if (U0 != U) {   // rare, and the same in every wave (both roles)
+      if constexpr (LIN) {
+        acc_scale<NB>(S, __builtin_ldexpf(1.0f, U - U0));
+        publish_state<NB>(L, S, OB::first, r, h);
+        stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -U0));
+        stage_write_v(cv, vtab(L, c0 & 1), lane, W);
+        if constexpr (LAYER) {
+          if (W == 0 && lane == 0) L.Us[c0 & 1] = U0;
+        }
+      } else {
+        sw.prev_v(L, p, c0, U0, W, lane);   // the previous 64 tokens' V again, with U0
+      }
       U = U0;
-      publish_state<NB>(L, S, OB::first, r, h);
-      stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -U));
-      stage_write_v(cv, L.VT, lane, W);
       lds_barrier();
     }
   }
@@ -985,6 +1215,14 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
   constexpr u32 kOnes = 0x3c003c00u;
   for (int c = 0; c < nch; ++c) {
     const int row0 = (c0 + c) * CH;
+    const bool more = c + 1 < nch;
+    if constexpr (!LIN) {
+      sw.phase1(L, p, c0 + c, W, lane, more);
+      lds_barrier();   // the recurrence waves' barrier after their chunk (same position)
+      sw.template phase2<OUT_F32>(L, p, c0 + c, W, lane, more);
+      if (more) lds_barrier();
+      continue;
+    }
     // max |S| of the state this chunk starts from (its MFMAs have completed: it was published)
     const u32 msS = wave_max_u32(acc_absmax<NB>(S));
     // next chunk, issued unconditionally (one basic block); after the last chunk it reads nothing
@@ -1074,7 +1312,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
         const u32x4 bp = {pk[4 * s], pk[4 * s + 1], pk[4 * s + 2], pk[4 * s + 3]};
 #pragma unroll
         for (int n = 0; n < 2; ++n) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(&L.VT[vt_off(32 * n + r, 4 * j + 2 * s + h)]);
+          const u32x4 a = *reinterpret_cast<const u32x4*>(&vtab(L, (c0 + c) & 1)[vt_off(32 * n + r, 4 * j + 2 * s + h)]);
           O[n] = mfma32x32x16_f16(a, bp, O[n]);
         }
       }
@@ -1090,7 +1328,15 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
       // v_rcp_f32 (1 ulp) instead of an IEEE division, and a select, keep this branch-free
       const float sc = p.normalize ? un * __builtin_amdgcn_rcpf(den + p.eps) : un;
       const int row = row0 + 32 * W + r;
-      if (VEC) {
+      if constexpr (LAYER) {
+        // handed to the softmax wave of these queries, which adds its branch and stores
+#pragma unroll
+        for (int n = 0; n < 2; ++n)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj)
+            *reinterpret_cast<f32x4*>(&L.YL[(32 * W + r) * YLS + 32 * n + 8 * jj + 4 * h]) =
+                (f32x4){O[n][4 * jj] * sc, O[n][4 * jj + 1] * sc, O[n][4 * jj + 2] * sc, O[n][4 * jj + 3] * sc};
+      } else if (VEC) {
         const __amdgpu_buffer_rsrc_t ro =
             make_rsrc(static_cast<char*>(p.out) + ((size_t)hrow + row0) * dv * esz, (u32)(N - row0) * (u32)dv * (u32)esz);
 #pragma unroll
@@ -1130,9 +1376,8 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
     }
 
     // ---- state update with this chunk
-    update_blocks<NB>(L.KT, L.VT, S, ra, rb, r, h);
+    update_blocks<NB>(L.KT, vtab(L, (c0 + c) & 1), S, ra, rb, r, h);
     if (GRAM) gram_update(L.KT, G, grow, h, 0, 1);
-    const bool more = c + 1 < nch;
     // next chunk in registers (V with the current exponent), and the maxima that decide the
     // next exponent: |S| before this update, |v| and |k| of the next chunk
     stage_convert_qk<true>(st, cv, p.qs, p.ks, lane);
@@ -1150,7 +1395,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
 
     lds_barrier();   // every wave is done with this chunk's tables and the published state
     if (more) {
-      stage_write<true>(cv, L.Q0, L.Kr, L.KT, L.VT, lane, W);
+      stage_write<true>(cv, L.Q0, L.Kr, L.KT, vtab(L, (c0 + c + 1) & 1), lane, W);
       publish_state<NB>(L, S, OB::first, r, h);
       if (GRAM) publish_gram(L, G, r, h);
     }
@@ -1172,7 +1417,7 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
         if (Un != U) acc_scale<NB>(S, __builtin_ldexpf(1.0f, U - Un));
         if (more) {
           stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -Un));
-          stage_write_v(cv, L.VT, lane, W);
+          stage_write_v(cv, vtab(L, (c0 + c + 1) & 1), lane, W);
           if (Un != U) publish_state<NB>(L, S, OB::first, r, h);
         }
         U = Un;
@@ -1180,12 +1425,15 @@ __device__ __forceinline__ void output_wave(OutLds& L, const ChunkParams& p, int
       eVc = eV;
       eKc = eK;
     }
+    if constexpr (LAYER) {
+      if (W == 0 && lane == 0 && more) L.Us[(c0 + c + 1) & 1] = U;   // exponent of the next chunk's V^T
+    }
     if (more) lds_barrier();
   }
 
   // ---- final state of the head (last segment) in the reference feature basis, fp32:
   // state_out[f][0..dv) = sum_u phi_f(k_u) v_u, state_out[f][dv] = sum_u phi_f(k_u)
-  if (p.state_out != nullptr && seg == p.P - 1) {
+  if (!LAYER && p.state_out != nullptr && seg == p.P - 1) {
     float* so = p.state_out + (size_t)bh * 153 * (dv + 1);
     // the Gram matrix in fp32 for the k-sums: G32[i][j], 32 x 33 floats over the S^T table
     float* G32 = reinterpret_cast<float*>(L.ST);
@@ -1240,6 +1488,26 @@ __global__ __launch_bounds__(64 * NWAVE_OUT, 2) void chunked_output_kernel(const
   }
 }
 
+// Kernel 3 of the full layer: outputs of both branches, one work-group of 8 waves per (head,
+// segment) (recurrence roles 0..3, softmax roles 4..7).
+template <bool OUT_F32, int DSW>
+__global__ __launch_bounds__(64 * 2 * NWAVE_OUT, 1) void chunked_layer_kernel(const ChunkParams p) {
+  __shared__ __attribute__((aligned(16))) LayerLds<DSW> L;
+  using LT = LayerLds<DSW>;
+  int bh, seg;
+  map_segment(blockIdx.x, p.BH, p.P, bh, seg);
+  switch (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) {
+    case 0: output_wave<0, true, OUT_F32, LT, DSW>(L, p, bh, seg); break;
+    case 1: output_wave<1, true, OUT_F32, LT, DSW>(L, p, bh, seg); break;
+    case 2: output_wave<2, true, OUT_F32, LT, DSW>(L, p, bh, seg); break;
+    case 3: output_wave<3, true, OUT_F32, LT, DSW>(L, p, bh, seg); break;
+    case 4: output_wave<4, true, OUT_F32, LT, DSW>(L, p, bh, seg); break;
+    case 5: output_wave<5, true, OUT_F32, LT, DSW>(L, p, bh, seg); break;
+    case 6: output_wave<6, true, OUT_F32, LT, DSW>(L, p, bh, seg); break;
+    default: output_wave<7, true, OUT_F32, LT, DSW>(L, p, bh, seg); break;
+  }
+}
+
 // Segment split: enough (head, segment) work-groups to fill the GPU twice over, at most
 // MAX_SEG segments per head.
 void segment_split(int BH, int N, int& P, int& seg_chunks) {
@@ -1273,31 +1541,32 @@ size_t chunked_scratch_bytes(int BH, int N, int d, int dv, bool with_state) {
   return chunked_workspace_bytes(BH, N, d, dv, 1);
 }
 
-int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
-  if (a.d != 16 || a.dv > 64) return LA_ERR_UNSUPPORTED_DIM;
-  if (a.in_f32) return LA_ERR_BAD_DTYPE;
-  if ((reinterpret_cast<uintptr_t>(a.q) & 7) || (reinterpret_cast<uintptr_t>(a.k) & 7)) return LA_ERR_BAD_ALIGNMENT;
+namespace {
+
+// Parameters of the chunked kernels shared by the chunked call and the full layer; P, seg_chunks
+// and the workspace pointers from the segment split.
+ChunkParams chunk_params(const void* q, const void* k, const void* v, void* out, void* workspace, int BH, int N,
+                         int dv, float scale) {
   ChunkParams p{};
-  p.q = static_cast<const uint16_t*>(a.q);
-  p.k = static_cast<const uint16_t*>(a.k);
-  p.v = static_cast<const uint16_t*>(a.v);
-  p.out = a.out;
-  p.state_out = a.state_out;
-  p.BH = a.BH;
-  p.N = a.N;
-  p.dv = a.dv;
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.out = out;
+  p.BH = BH;
+  p.N = N;
+  p.dv = dv;
   int P, seg_chunks;
-  segment_split(a.BH, a.N, P, seg_chunks);
+  segment_split(BH, N, P, seg_chunks);
   p.P = P;
   p.seg_chunks = seg_chunks;
-  const size_t nslot = (size_t)a.BH * P;
-  char* ws = static_cast<char*>(a.workspace);
+  const size_t nslot = (size_t)BH * P;
+  char* ws = static_cast<char*>(workspace);
   p.wsS = reinterpret_cast<uint16_t*>(ws);
   p.wsG = reinterpret_cast<float*>(ws + nslot * 64 * NF * 2);
   p.wsE = reinterpret_cast<int*>(ws + nslot * (64 * NF * 2 + 1024 * 4));
   p.wsEP = p.wsE + nslot;
   // q~ = sqrt(scale) q (q~.k~ = s); the K^T table rows hold k~/2
-  const double rc = sqrt((double)a.scale);
+  const double rc = sqrt((double)scale);
   p.qs = (float)rc;
   p.ks = (float)(0.5 * rc);
   // k side of 2p -> reference features: constant 2, linear k~, square k~^2, pair k~ k~
@@ -1306,20 +1575,19 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
   p.st_fac[2] = (float)(1.0 / sqrt(2.0));
   p.st_fac[3] = 1.0f;
   for (int i = 0; i < 4; ++i) p.st_inv[i] = (float)(1.0 / (double)p.st_fac[i]);
-  p.state_in = a.state_in;
-  p.prev_tokens = (float)a.prev_tokens;
-  p.eps = a.eps;
-  p.normalize = a.normalize ? 1 : 0;
-  p.out_f32 = a.out_f32 ? 1 : 0;
-  const bool vec_v = (a.dv % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 15) == 0);
-  p.vec_out = (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0);
-  if (a.state_in != nullptr) {
-    hipLaunchKernelGGL(chunked_import_kernel, dim3((unsigned)a.BH), dim3(256), 0, stream, p);
+  return p;
+}
+
+// Kernels 1 and 2 (state increments of every segment but the last, their prefixes); the
+// initial-state import before them when p.state_in is set.
+int launch_increments(const ChunkParams& p, bool vec_v, hipStream_t stream) {
+  if (p.state_in != nullptr) {
+    hipLaunchKernelGGL(chunked_import_kernel, dim3((unsigned)p.BH), dim3(256), 0, stream, p);
     const int e = (int)hipGetLastError();
     if (e != 0) return e;
   }
-  if (P > 1) {
-    const dim3 grid((unsigned)((a.BH * (P - 1) + SEG_PER_WG - 1) / SEG_PER_WG));
+  if (p.P > 1) {
+    const dim3 grid((unsigned)((p.BH * (p.P - 1) + SEG_PER_WG - 1) / SEG_PER_WG));
     const dim3 block(64 * NWAVE_SEG * SEG_PER_WG);
     if (vec_v)
       hipLaunchKernelGGL(chunked_segment_kernel<true>, grid, block, 0, stream, p);
@@ -1327,12 +1595,32 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
       hipLaunchKernelGGL(chunked_segment_kernel<false>, grid, block, 0, stream, p);
     int e = (int)hipGetLastError();
     if (e != 0) return e;
-    const dim3 pgrid((unsigned)((64 * NF / 4 + 1024 / 2 + 255) / 256), (unsigned)a.BH);
+    const dim3 pgrid((unsigned)((64 * NF / 4 + 1024 / 2 + 255) / 256), (unsigned)p.BH);
     hipLaunchKernelGGL(chunked_prefix_kernel, pgrid, dim3(256), 0, stream, p);
     e = (int)hipGetLastError();
     if (e != 0) return e;
   }
-  const dim3 grid((unsigned)(a.BH * P));
+  return 0;
+}
+
+}  // namespace
+
+int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
+  if (a.d != 16 || a.dv > 64) return LA_ERR_UNSUPPORTED_DIM;
+  if (a.in_f32) return LA_ERR_BAD_DTYPE;
+  if ((reinterpret_cast<uintptr_t>(a.q) & 7) || (reinterpret_cast<uintptr_t>(a.k) & 7)) return LA_ERR_BAD_ALIGNMENT;
+  ChunkParams p = chunk_params(a.q, a.k, a.v, a.out, a.workspace, a.BH, a.N, a.dv, a.scale);
+  p.state_out = a.state_out;
+  p.state_in = a.state_in;
+  p.prev_tokens = (float)a.prev_tokens;
+  p.eps = a.eps;
+  p.normalize = a.normalize ? 1 : 0;
+  p.out_f32 = a.out_f32 ? 1 : 0;
+  const bool vec_v = (a.dv % 8 == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 15) == 0);
+  p.vec_out = (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0);
+  const int e = launch_increments(p, vec_v, stream);
+  if (e != 0) return e;
+  const dim3 grid((unsigned)(a.BH * p.P));
   const dim3 block(64 * NWAVE_OUT);
   const bool vec = vec_v && p.vec_out;
   if (vec && a.out_f32)
@@ -1343,6 +1631,36 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((chunked_output_kernel<false, true>), grid, block, 0, stream, p);
   else
     hipLaunchKernelGGL((chunked_output_kernel<false, false>), grid, block, 0, stream, p);
+  return (int)hipGetLastError();
+}
+
+bool layer_fused_shape(int d, int dv, int dsw, int window) {
+  return d == 16 && dv % 8 == 0 && dv <= 64 && (dsw == 16 || dsw == 32 || dsw == 64) && window >= 1 && window <= 64;
+}
+
+int launch_based_layer(const LayerArgs& a, hipStream_t stream) {
+  if (!layer_fused_shape(a.d, a.dv, a.dsw, a.window)) return LA_ERR_UNSUPPORTED_DIM;
+  ChunkParams p = chunk_params(a.q, a.k, a.v, a.out, a.workspace, a.BH, a.N, a.dv, a.scale);
+  p.eps = a.eps;
+  p.normalize = 1;
+  p.out_f32 = a.out_f32 ? 1 : 0;
+  p.vec_out = 1;
+  p.qsw = static_cast<const uint16_t*>(a.qsw);
+  p.ksw = static_cast<const uint16_t*>(a.ksw);
+  p.window = a.window;
+  p.sw_log2 = (float)((double)a.scale_sw * 1.4426950408889634);
+  const int e = launch_increments(p, true, stream);
+  if (e != 0) return e;
+  const dim3 grid((unsigned)(a.BH * p.P)), block(64 * 2 * NWAVE_OUT);
+#define LA_LAYER(F32, D) hipLaunchKernelGGL((chunked_layer_kernel<F32, D>), grid, block, 0, stream, p)
+  if (a.dsw == 16) {
+    if (a.out_f32) LA_LAYER(true, 16); else LA_LAYER(false, 16);
+  } else if (a.dsw == 32) {
+    if (a.out_f32) LA_LAYER(true, 32); else LA_LAYER(false, 32);
+  } else {
+    if (a.out_f32) LA_LAYER(true, 64); else LA_LAYER(false, 64);
+  }
+#undef LA_LAYER
   return (int)hipGetLastError();
 }
 

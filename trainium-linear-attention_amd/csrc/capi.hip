@@ -188,6 +188,45 @@ static int chunked_common(const void* q, const void* k, const void* v, int in_dt
   return la::launch_based_chunked(a, static_cast<hipStream_t>(hip_stream));
 }
 
+int la_based_layer_fwd(const void* q, const void* k, const void* v, const void* q_sw, const void* k_sw,
+                       int in_dtype, void* out, int out_dtype, int B, int H, int N, int d, int dv, int d_sw,
+                       int window, float scale, float scale_sw, float eps, void* workspace,
+                       size_t workspace_bytes, void* hip_stream) {
+  int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
+  if (rc != LA_OK) return rc;
+  if (q_sw == nullptr || k_sw == nullptr) return LA_ERR_NULL_POINTER;
+  if (in_dtype != LA_BF16) return LA_ERR_BAD_DTYPE;
+  if (!la::layer_fused_shape(d, dv, d_sw, window)) return LA_ERR_UNSUPPORTED_DIM;
+  if (!finite_f(scale) || !(scale > 0.f) || !finite_f(scale_sw) || !(scale_sw > 0.f) || !finite_f(eps) || eps < 0.f)
+    return LA_ERR_BAD_SCALAR;
+  if ((long long)B * H * N == 0) return LA_OK;
+  if (!al(q, 16) || !al(k, 16) || !al(v, 16) || !al(q_sw, 16) || !al(k_sw, 16) || !al(out, 16))
+    return LA_ERR_BAD_ALIGNMENT;
+  const size_t need = la::chunked_scratch_bytes(B * H, N, d, dv, false);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
+  if (need > 0 && !al(workspace, 16)) return LA_ERR_BAD_ALIGNMENT;
+  la::LayerArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.qsw = q_sw;
+  a.ksw = k_sw;
+  a.out = out;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  a.BH = B * H;
+  a.N = N;
+  a.d = d;
+  a.dv = dv;
+  a.dsw = d_sw;
+  a.window = window;
+  a.scale = scale;
+  a.scale_sw = scale_sw;
+  a.eps = eps;
+  a.out_f32 = out_dtype == LA_F32;
+  return la::launch_based_layer(a, static_cast<hipStream_t>(hip_stream));
+}
+
 int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
                          int H, int N, int d, int dv, int chunk, float scale, float eps, int normalize,
                          void* workspace, size_t workspace_bytes, float* state_out_or_null, void* hip_stream) {

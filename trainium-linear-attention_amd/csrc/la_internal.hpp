@@ -51,6 +51,20 @@ struct ChunkedArgs {
   bool in_f32, out_f32;
 };
 
+struct LayerArgs {
+  const void* q;       // linear branch (d = 16)
+  const void* k;
+  const void* v;
+  const void* qsw;     // softmax branch (dsw)
+  const void* ksw;
+  void* out;
+  void* workspace;     // chunked_workspace_bytes()
+  size_t workspace_bytes;
+  int BH, N, d, dv, dsw, window;
+  float scale, scale_sw, eps;
+  bool out_f32;
+};
+
 struct IdentityArgs {
   const void* q;
   const void* k;
@@ -96,6 +110,8 @@ int chunked_chunk_tokens();   // tokens per chunk of the chunked kernels
 // segment and there is no initial state, (size_t)-1 for unsupported shapes.
 size_t chunked_scratch_bytes(int BH, int N, int d, int dv, bool with_state);
 int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream);
+bool layer_fused_shape(int d, int dv, int dsw, int window);   // shapes of chunked_layer_kernel
+int launch_based_layer(const LayerArgs& a, hipStream_t stream);
 int launch_feature_map(const FeatureMapArgs& a, hipStream_t stream);
 int device_cu_count();   // compute units of the current device (256 when the query fails)
 bool identity_shape(int d, int dv);

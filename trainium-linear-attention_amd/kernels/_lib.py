@@ -54,6 +54,9 @@ _SIGNATURES = {
     "la_based_chunked_fwd_continue": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
                                                _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int, _c_void,
                                                _c_size, _c_void, ctypes.c_longlong, _c_void, _c_void]),
+    "la_based_layer_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int,
+                                    _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_float,
+                                    _c_void, _c_size, _c_void]),
     "la_based_decode_step": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int, _c_int,
                                       _c_int, _c_int, _c_float, _c_int, _c_void]),
     "la_based_decode_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
@@ -65,7 +68,7 @@ _SIGNATURES = {
     "la_taylor_feature_map": (_c_int, [_c_void, _c_int, _c_void, _c_int, ctypes.c_longlong, _c_int, _c_void]),
 }
 
-EXPECTED_ABI = 7
+EXPECTED_ABI = 8
 
 
 class BasedLAError(RuntimeError):
