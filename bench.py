@@ -75,6 +75,9 @@ def parse():
     ap.add_argument("--identity", action="store_true",
                     help="only time the identity-map linear attention numerator (la_identity_linear_fwd) at "
                          "B2 H16 N8192 d16 dv64 bf16 against its HBM roofline")
+    ap.add_argument("--clock-transient", action="store_true",
+                    help="only time single calls of the headline attention kernel: 60 back to back from idle, then 20 "
+                         "after 20 ms idle gaps (the step from idle to load that --settle-ms waits out)")
     ap.add_argument("--crossover", action="store_true",
                     help="only sweep sequence lengths: whole parallel forward vs chunked forward (d=16, dv=64, bf16), "
                          "the measurement behind solution()'s dispatch threshold")
@@ -258,6 +261,38 @@ def measure(cfg, steps, warmup, rotate, device, main_only=False):
 # (B, H) pairs and sequence lengths of the crossover sweep (the reference sweeps 256 .. 16384 at B=1, H=2)
 CROSSOVER_BH = [(1, 2), (2, 16), (8, 16)]
 CROSSOVER_N = [256, 512, 1024, 2048, 4096, 8192, 16384]
+
+
+def clock_transient(device):
+    """Per-call microseconds of the headline attention kernel (V pre-pass done once): 60 calls
+    back to back after 0.5 s idle, then 20 calls each after a 20 ms idle gap."""
+    import torch
+
+    name, kind, B, H, N, d, dv, dt, seed, chunk, window, prescale = HEADLINE
+    q, k, v = make_inputs(B, H, N, d, dv, dt, seed, prescale, device)
+    call = Call(kind, q, k, v, chunk, window, main_only=True)
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+
+    def per_call(n, gap_s):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for a, b in ev:
+            if gap_s:
+                torch.cuda.synchronize()
+                time.sleep(gap_s)
+            a.record()
+            call()
+            b.record()
+        torch.cuda.synchronize()
+        return [round(a.elapsed_time(b) * 1000, 1) for a, b in ev]
+
+    time.sleep(0.5)
+    b2b = per_call(60, 0.0)
+    time.sleep(0.5)
+    gaps = per_call(20, 0.02)
+    return {"clock_transient": {"kernel": "based_parallel_bf16_kernel", "shape": "B2 H16 N8192 d16 dv64 bf16",
+                                "back_to_back_us": b2b, "after_20ms_idle_us": gaps}}
 
 
 def crossover(steps, warmup, rotate, device):
@@ -523,6 +558,10 @@ def main():
 
     if args.crossover:
         print(json.dumps(crossover(args.steps, args.warmup, args.rotate, device)))
+        return
+
+    if args.clock_transient:
+        print(json.dumps(clock_transient(device)))
         return
 
     if args.only:
