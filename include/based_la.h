@@ -110,7 +110,11 @@ int la_based_parallel_fwd_packed(const void* q, const void* k, const void* v, in
  * chunk: the reference's chunk_size, any value >= 1 (LA_ERR_BAD_SHAPE below 1).  The recurrence
  * computes the same function for every chunk size (chunk-size invariance); it runs in chunks of
  * la_based_chunked_chunk_used(chunk) tokens.
- * Limits: d == 16, 1 <= dv <= 64.
+ * Limits: bf16 inputs, 1 <= d <= 64, 1 <= dv <= 128.  d == 16 with dv <= 64 runs the chunk
+ * recurrence (128-token chunks, state export and import); other shapes run the segment-state
+ * path (state prefixes of 512-token segments in the feature basis, then each query against its
+ * segment's prefix plus the quadratic form inside the segment), which has no state export
+ * (LA_ERR_UNSUPPORTED_DIM with state_out_or_null set).  Both are linear in N.
  */
 size_t la_based_chunked_workspace_bytes(int B, int H, int N, int d, int dv, int chunk);
 

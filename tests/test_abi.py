@@ -325,8 +325,8 @@ def test_chunked_noalloc_argument_errors():
 
     assert call(q=None) == -1
     assert call(chunk=0) == -2
-    assert call(d=32) == -5
-    assert call(dv=65) == -5
+    assert call(d=65) == -5           # above the segment-state path's 64
+    assert call(dv=129) == -5
     assert call(N=0) == 0
     assert call(dt=5) == -3
     # largest scratch need below the limit: 511 heads x 2 segments of 24 KiB records

@@ -1525,7 +1525,8 @@ void segment_split(int BH, int N, int& P, int& seg_chunks) {
 int chunked_chunk_tokens() { return CH; }
 
 size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk) {
-  if (d != 16 || dv > 64 || chunk < 1) return (size_t)-1;
+  if (chunk < 1) return (size_t)-1;
+  if (d != 16 || dv > 64) return general_chunked_bytes(BH, N, d, dv, false);
   int P, seg_chunks;
   segment_split(BH, N, P, seg_chunks);
   // per (head, segment): fp16 S^T, fp32 Gram matrix, two exponents
@@ -1533,8 +1534,8 @@ size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk) {
   return (size_t)BH * P * per + 256;
 }
 
-size_t chunked_scratch_bytes(int BH, int N, int d, int dv, bool with_state) {
-  if (d != 16 || dv > 64) return (size_t)-1;
+size_t chunked_scratch_bytes(int BH, int N, int d, int dv, bool with_state, bool in_f32) {
+  if (d != 16 || dv > 64 || in_f32) return with_state ? (size_t)-1 : general_chunked_bytes(BH, N, d, dv, in_f32);
   int P, seg_chunks;
   segment_split(BH, N, P, seg_chunks);
   if (P == 1 && !with_state) return 0;
@@ -1606,8 +1607,11 @@ int launch_increments(const ChunkParams& p, bool vec_v, hipStream_t stream) {
 }  // namespace
 
 int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
-  if (a.d != 16 || a.dv > 64) return LA_ERR_UNSUPPORTED_DIM;
-  if (a.in_f32) return LA_ERR_BAD_DTYPE;
+  if (a.d != 16 || a.dv > 64 || a.in_f32) {
+    // other head dims and fp32 inputs: segment states + outputs; no state export or import
+    if (a.state_out != nullptr || a.state_in != nullptr) return LA_ERR_UNSUPPORTED_DIM;
+    return launch_general_chunked(a, stream);
+  }
   if ((reinterpret_cast<uintptr_t>(a.q) & 7) || (reinterpret_cast<uintptr_t>(a.k) & 7)) return LA_ERR_BAD_ALIGNMENT;
   ChunkParams p = chunk_params(a.q, a.k, a.v, a.out, a.workspace, a.BH, a.N, a.dv, a.scale);
   p.state_out = a.state_out;

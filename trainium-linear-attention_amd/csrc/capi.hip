@@ -152,7 +152,7 @@ static int chunked_common(const void* q, const void* k, const void* v, int in_dt
   if (!finite_f(scale) || !(scale > 0.f) || !finite_f(eps) || eps < 0.f) return LA_ERR_BAD_SCALAR;
   if (chunk < 1) return LA_ERR_BAD_SHAPE;
   if ((long long)B * H * N == 0) return LA_OK;
-  const size_t need = la::chunked_scratch_bytes(B * H, N, d, dv, state_in != nullptr);
+  const size_t need = la::chunked_scratch_bytes(B * H, N, d, dv, state_in != nullptr, in_dtype == LA_F32);
   if (need == (size_t)-1) return LA_ERR_UNSUPPORTED_DIM;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
   if (state_out_or_null != nullptr && (reinterpret_cast<uintptr_t>(state_out_or_null) & 3)) return LA_ERR_BAD_ALIGNMENT;
@@ -202,7 +202,7 @@ int la_based_layer_fwd(const void* q, const void* k, const void* v, const void* 
   if ((long long)B * H * N == 0) return LA_OK;
   if (!al(q, 16) || !al(k, 16) || !al(v, 16) || !al(q_sw, 16) || !al(k_sw, 16) || !al(out, 16))
     return LA_ERR_BAD_ALIGNMENT;
-  const size_t need = la::chunked_scratch_bytes(B * H, N, d, dv, false);
+  const size_t need = la::chunked_scratch_bytes(B * H, N, d, dv, false, false);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
   if (need > 0 && !al(workspace, 16)) return LA_ERR_BAD_ALIGNMENT;
   la::LayerArgs a{};
@@ -290,7 +290,7 @@ int la_based_chunked_fwd_noalloc(const void* q, const void* k, const void* v, in
   if (rc != LA_OK) return rc;
   if (chunk < 1) return LA_ERR_BAD_SHAPE;
   if ((long long)B * H * N == 0) return LA_OK;
-  const size_t need = la::chunked_scratch_bytes(B * H, N, d, dv, false);
+  const size_t need = la::chunked_scratch_bytes(B * H, N, d, dv, false, in_dtype == LA_F32);
   if (need == (size_t)-1) return LA_ERR_UNSUPPORTED_DIM;
   if (need > (size_t)LA_NOALLOC_SCRATCH_BYTES) return LA_ERR_SCRATCH_LIMIT;
   void* ws = nullptr;

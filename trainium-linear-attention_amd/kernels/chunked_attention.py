@@ -13,9 +13,12 @@ The feature map is applied inside the chunked kernel: phi(Q), phi(K) never reach
 state stays on chip across chunks (the NKI kernel round-trips it through HBM,
 kernels/nki_attention_chunked.py:92-102).  dv may differ from d.
 
-The chunked kernel covers bf16 inputs with d = 16 and dv <= 64 (the BASED configuration).
-Other shapes and fp32 inputs are computed by the fused parallel kernel, which evaluates the
-same function (numerator or normalised) on the GPU.  ``chunk_size`` is the reference's argument
+Two chunked paths: the recurrence kernel for bf16 inputs with d = 16 and dv <= 64 (the BASED
+configuration), and for other head dims (d <= 64, dv <= 128, bf16) a segment-state path (state
+prefixes of 512-token segments in the feature basis, then every query's contraction with its
+segment's prefix plus the quadratic form inside the segment).  Both are linear in the sequence
+length.  Shapes outside both are computed by the fused parallel kernel, which evaluates the same
+function (numerator or normalised) on the GPU.  ``chunk_size`` is the reference's argument
 (any value >= 1); the kernel's recurrence runs 128-token chunks (``la_based_chunked_chunk_used``
 reports it), which gives the same result for every chunk size up to rounding (chunk-size
 invariance of the recurrence).
@@ -31,8 +34,7 @@ from . import _lib
 from .pytorch_attention import _as_kernel_input, _check_qkv, _compute_dtype
 
 __all__ = ["taylor_feature_map", "feature_dim", "chunked_nki_numerator", "chunked_based_attn", "based_chunked",
-           "based_decode_step",
-           "chunked_supported"]
+           "based_decode_step", "chunked_supported", "general_chunked_supported"]
 
 
 def feature_dim(d: int) -> int:
@@ -55,8 +57,14 @@ def taylor_feature_map(x):
 
 
 def chunked_supported(d: int, dv: int, dtype: torch.dtype) -> bool:
-    """Shapes the chunked HIP kernel implements (bf16, d = 16, dv <= 64)."""
+    """Shapes the chunk-recurrence kernel implements (bf16, d = 16, dv <= 64); it also exports
+    and imports states."""
     return d == 16 and 1 <= dv <= 64 and dtype == torch.bfloat16
+
+
+def general_chunked_supported(d: int, dv: int, dtype: torch.dtype) -> bool:
+    """Shapes of the segment-state chunked path (bf16, d <= 64, dv <= 128), linear in N."""
+    return 1 <= d <= 64 and 1 <= dv <= 128 and dtype == torch.bfloat16
 
 
 def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, out_dtype=None,
@@ -78,8 +86,9 @@ def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, 
     if not chunked_supported(d, dv, cdt):
         if return_state or state_in is not None:
             raise _lib.BasedLAError("state export and import need the chunked kernel (bf16, d = 16, dv <= 64)")
-        from .pytorch_attention import based_parallel
-        return based_parallel(q, k, v, eps=eps, scale=scale, normalize=normalize, out_dtype=out_dtype)
+        if not general_chunked_supported(d, dv, cdt):
+            from .pytorch_attention import based_parallel
+            return based_parallel(q, k, v, eps=eps, scale=scale, normalize=normalize, out_dtype=out_dtype)
     odt = q.dtype if out_dtype is None else out_dtype
     kdt = odt if odt in (torch.float32, torch.bfloat16) else torch.float32
     if scale is None:

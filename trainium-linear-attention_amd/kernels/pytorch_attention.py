@@ -122,15 +122,25 @@ def ref_based_attn(q, k, v, eps=1e-6):
 # fused kernel.
 CHUNKED_MIN_T = 256
 
+# Sequence length from which ``solution`` uses the segment-state chunked path for the other head
+# dims (d <= 64, dv <= 128, bf16).  Measured on MI355X at B2 H16 d64 dv64 bf16: 0.513 ms against
+# 0.444 ms for the fused kernel at N = 8192, 3.2 ms at B1 H16 N = 65536, where the fused kernel's
+# quadratic work is 32 times that at N = 8192 for half the heads.
+GENERAL_CHUNKED_MIN_T = 16384
+
 
 def solution(q, k, v, eps=1e-6):
     """BASED causal attention (reference :81-92).
 
-    Dispatches by sequence length between the parallel fused kernel and the chunked
-    recurrent kernel, which compute the same function; shapes the chunked kernel does not
-    take (d != 16, dv > 64, fp32) go to the fused kernel.  There is no PyTorch fallback.
+    Dispatches by sequence length between the parallel fused kernel and the chunked kernels,
+    which compute the same function: the d = 16 recurrence kernel from ``CHUNKED_MIN_T`` tokens,
+    the segment-state path for other head dims from ``GENERAL_CHUNKED_MIN_T``; fp32 inputs and
+    other shapes go to the fused kernel.  There is no PyTorch fallback.
     """
-    if q.shape[-2] >= CHUNKED_MIN_T:
-        from .chunked_attention import chunked_based_attn
+    from .chunked_attention import chunked_based_attn, chunked_supported, general_chunked_supported
+    t, d, dv = q.shape[-2], q.shape[-1], v.shape[-1]
+    cdt = _compute_dtype(q.dtype)
+    if (t >= CHUNKED_MIN_T and chunked_supported(d, dv, cdt)) or (
+            t >= GENERAL_CHUNKED_MIN_T and general_chunked_supported(d, dv, cdt)):
         return chunked_based_attn(q, k, v, eps=eps)
     return based_parallel(q, k, v, eps=eps)
