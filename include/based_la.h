@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 8
+#define LA_ABI_VERSION 9
 
 /* element types */
 #define LA_F32 0
@@ -110,13 +110,21 @@ int la_based_parallel_fwd_packed(const void* q, const void* k, const void* v, in
  * chunk: the reference's chunk_size, any value >= 1 (LA_ERR_BAD_SHAPE below 1).  The recurrence
  * computes the same function for every chunk size (chunk-size invariance); it runs in chunks of
  * la_based_chunked_chunk_used(chunk) tokens.
- * Limits: bf16 inputs, 1 <= d <= 64, 1 <= dv <= 128.  d == 16 with dv <= 64 runs the chunk
- * recurrence (128-token chunks, state export and import); other shapes run the segment-state
- * path (state prefixes of 512-token segments in the feature basis, then each query against its
- * segment's prefix plus the quadratic form inside the segment), which has no state export
- * (LA_ERR_UNSUPPORTED_DIM with state_out_or_null set).  Both are linear in N.
+ * Limits: 1 <= d <= 64, 1 <= dv <= 128.  bf16 inputs with d == 16 and dv <= 64 run the chunk
+ * recurrence (128-token chunks, state export and import); other shapes and fp32 inputs run the
+ * segment-state path (state prefixes of 512-token segments in the feature basis, then each query
+ * against its segment's prefix plus the quadratic form inside the segment; fp32 arithmetic
+ * throughout for fp32 inputs), which has no state export (LA_ERR_UNSUPPORTED_DIM with
+ * state_out_or_null set).  Both are linear in N.
  */
 size_t la_based_chunked_workspace_bytes(int B, int H, int N, int d, int dv, int chunk);
+
+/*
+ * The same for one input type (LA_BF16 or LA_F32; (size_t)-1 for others): the scratch the
+ * chunked entry points need for inputs of that type, which for fp32 inputs is the segment-state
+ * path's fp32 state prefixes.  la_based_chunked_workspace_bytes returns the larger of the two.
+ */
+size_t la_based_chunked_workspace_bytes_dt(int B, int H, int N, int d, int dv, int chunk, int in_dtype);
 
 /*
  * Tokens per chunk the chunked kernels run for a requested chunk size (128 for every chunk >= 1;

@@ -26,7 +26,8 @@ def _lib():
 def test_header_declares_expected_entry_points():
     assert _declared() == sorted([
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
-        "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes", "la_based_chunked_chunk_used", "la_based_chunked_fwd",
+        "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes",
+        "la_based_chunked_workspace_bytes_dt", "la_based_chunked_chunk_used", "la_based_chunked_fwd",
         "la_based_chunked_fwd_continue", "la_based_chunked_fwd_noalloc", "la_sliding_window_fwd",
         "la_sliding_window_fwd_add", "la_based_layer_fwd", "la_based_decode_step", "la_based_decode_workspace_bytes",
         "la_based_decode_step_ws", "la_identity_workspace_bytes", "la_identity_linear_fwd",
@@ -41,7 +42,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib()
-    assert lib.la_abi_version() == 8
+    assert lib.la_abi_version() == 9
     for code in range(-10, 1):
         s = lib.la_status_string(code).decode()
         assert s and s != "unknown status"
@@ -330,7 +331,7 @@ def test_chunked_noalloc_argument_errors():
     assert call(N=0) == 0
     assert call(dt=5) == -3
     # largest scratch need below the limit: 511 heads x 2 segments of 24 KiB records
-    assert lib.la_based_chunked_workspace_bytes(1, 511, 256, 16, 64, 64) <= (32 << 20)
+    assert lib.la_based_chunked_workspace_bytes_dt(1, 511, 256, 16, 64, 64, 1) <= (32 << 20)
 
 
 def test_lds_copy_carries_its_wait_states():
@@ -384,3 +385,18 @@ def test_python_wrappers_refuse_cpu_tensors():
         kernels.chunked_nki_numerator(q, q, q)
     with pytest.raises(RuntimeError):
         kernels.taylor_feature_map(q)
+
+
+def test_chunked_workspace_by_dtype():
+    """The workspace query per input type: the bf16 d = 16 recurrence's, the segment-state path's
+    for other head dims and for fp32 (its fp32 prefixes); the legacy query covers both types;
+    one-segment sequences need none on the segment-state path."""
+    lib = _lib()
+    f, g = lib.la_based_chunked_workspace_bytes_dt, lib.la_based_chunked_workspace_bytes
+    b16 = f(2, 16, 8192, 16, 64, 64, 1)
+    f32 = f(2, 16, 8192, 16, 64, 64, 0)
+    assert 0 < b16 < f32 and g(2, 16, 8192, 16, 64, 64) == max(b16, f32)
+    assert f(2, 16, 512, 64, 64, 64, 1) == 0 and f(2, 16, 512, 64, 64, 64, 0) == 0   # one segment
+    assert f(1, 1, 1025, 64, 128, 64, 0) > f(1, 1, 1025, 64, 128, 64, 1) > 0
+    assert f(1, 1, 8192, 65, 64, 64, 1) == (1 << 64) - 1       # above the path's d
+    assert f(1, 1, 8192, 16, 64, 64, 7) == (1 << 64) - 1       # unknown type

@@ -112,3 +112,36 @@ def test_solution_takes_general_path_for_long_sequences():
     assert ref.rel_err(y32[0, 0, rows], rows_fp64(q, k, v, 0, 0, rows)) < TOL
     ys = K.solution(qd[:, :, :300], kd[:, :, :300], vd[:, :, :300])
     assert torch.equal(ys, K.solution_nki(qd[:, :, :300], kd[:, :, :300], vd[:, :, :300]))
+
+
+TOL_F32 = 1e-4
+
+
+@pytest.mark.parametrize("N", [1, 100, 511, 512, 513, 1025, 2500])
+@pytest.mark.parametrize("d,dv", [(16, 64), (64, 64), (32, 128), (5, 96), (48, 40)])
+def test_general_f32_matches_oracle(N, d, dv):
+    """fp32 inputs on the segment-state path (fp32 features, states and sums; fp32 MFMAs)
+    against the fp64 oracle at the fp32 bar, normalised and numerator."""
+    K = _kernels()
+    q, k, v = rand_qkv(1, 2, N, d, dv, seed=N + 3 * d + dv, dtype=torch.float32)
+    qd, kd, vd = to_dev(q, k, v)
+    y = K.based_chunked(qd, kd, vd)
+    num = K.based_chunked(qd, kd, vd, normalize=False)
+    assert y.dtype == torch.float32
+    want, want_num, _ = ref.based_dense(q, k, v)
+    e, en = err(y, want), err(num, want_num)
+    print(f"fp32 N={N} d={d} dv={dv} err={e:.3e} num_err={en:.3e}")
+    assert e < TOL_F32 and en < TOL_F32
+
+
+def test_general_f32_wrappers():
+    """chunked_nki_numerator at fp32 (the reference's chunked kernel takes fp32 inputs,
+    kernels/nki_attention_chunked.py:27-33) over six heads, and a bf16 output of fp32 inputs."""
+    K = _kernels()
+    q, k, v = rand_qkv(2, 3, 1200, 16, 64, seed=4, dtype=torch.float32)
+    qd, kd, vd = to_dev(q, k, v)
+    want, want_num, _ = ref.based_dense(q, k, v)
+    num = K.chunked_nki_numerator(qd, kd, vd, chunk_size=64)
+    assert num.dtype == torch.float32 and max(head_errs(num, want_num)) < TOL_F32
+    yb = K.based_chunked(qd, kd, vd, out_dtype=torch.bfloat16)
+    assert torch.equal(yb, K.based_chunked(qd, kd, vd).to(torch.bfloat16))

@@ -135,6 +135,16 @@ int la_based_parallel_fwd_packed(const void* q, const void* k, const void* v, in
 
 size_t la_based_chunked_workspace_bytes(int B, int H, int N, int d, int dv, int chunk) {
   if (B < 1 || H < 1 || N < 1 || d < 1 || dv < 1 || chunk < 1) return 0;
+  const size_t b16 = la::chunked_workspace_bytes(B * H, N, d, dv, chunk);
+  const size_t f32 = la::general_chunked_bytes(B * H, N, d, dv, true);
+  if (b16 == (size_t)-1 || f32 == (size_t)-1) return b16 == (size_t)-1 ? f32 : b16;
+  return b16 > f32 ? b16 : f32;   // enough for either input type
+}
+
+size_t la_based_chunked_workspace_bytes_dt(int B, int H, int N, int d, int dv, int chunk, int in_dtype) {
+  if (B < 1 || H < 1 || N < 1 || d < 1 || dv < 1 || chunk < 1) return 0;
+  if (in_dtype == LA_F32) return la::general_chunked_bytes(B * H, N, d, dv, true);
+  if (in_dtype != LA_BF16) return (size_t)-1;
   return la::chunked_workspace_bytes(B * H, N, d, dv, chunk);
 }
 

@@ -2,27 +2,18 @@
 // dv <= 128, bf16 inputs.  Linear in N: the sequence is cut into segments of GL tokens; the
 // tokens of a segment see the earlier segments through their state and each other through the
 // quadratic form, as the chunk recurrence of kernels/nki_attention_chunked.py:65-109 with
-// chunk = GL (the recurrence gives the same function for every chunk size).
+// chunk = GL (the recurrence gives the same function for every chunk size).  The feature basis
+// (block-symmetric groups over [k, 1]) is described in la_general.hpp.
 //
-// Feature basis.  With a' = [scale q, 1] and b' = [k, 1], a'.b' = 1 + s, so
-// p(s) = 1 + s + s^2/2 = 1/2 (a'.b')^2 + 1/2 = 1/2 sum_ij a'_i a'_j b'_i b'_j + 1/2.
-// The pairs (i, j) are grouped in 16-wide blocks of j over the dims padded to DP = 16 ceil(d/16)
-// plus the augmented index DP (the 1), keeping the upper block triangle:
-//   quad groups   (i, J)  i < DP, J = i/16 .. DB-1   features a_i a_j, j in block J,
-//                                                     weight 1/2 on the diagonal block, 1 above
-//   linear groups (DP, J) J < DB                      features a_j,       weight 1
-//   constant      (DP, DB)                            feature 1 (j = DP), weight 1
-// (DB = DP/16), in i-major order.  With T_f = sum_u b'_i(u) b'_j(u) v_u and z_f = sum_u b'_i b'_j
-// over the tokens u of the earlier segments, a query's numerator is sum_f w_f a'_i a'_j T_f and
-// its denominator sum_f w_f a'_i a'_j z_f; the weights carry the 1/2, the symmetry of the
-// off-diagonal blocks and the extra 1/2 of the constant.
-//
+// Kernel 0 (gprep_kernel) converts every 64-token chunk before the last segment once: per-token
+// normalised fp16 k~^T rows, v n^2 rows and the n^2 row with the chunk's exponents.
 // Kernel 1 (gstate_kernel): one work-group per (head, 16 groups); its four waves hold two
-// 32-feature tiles each as fp32 MFMA accumulators over dv and sweep the head's segments in
-// 64-token chunks: A = feature rows (products b'_i b'_j formed in fp32 from LDS, rounded to
-// bf16), B = V (bf16, transposed in LDS), K = tokens.  After every segment but the last it
-// writes the state so far, the exclusive prefix of the next segment, as fp16 with one exponent
-// per (segment, work-group), and z from the same rounded products.
+// 32-feature tiles each as fp32 MFMA accumulators over dv and sweep the head's converted chunks
+// through an LDS ring (buffer_load ... lds, NS - 1 chunks ahead): A = feature rows (one
+// v_pk_mul_f16 per two products k~_i k~_j), B = the V^T rows, K = tokens, fp16 MFMAs; z from the
+// same products against the n^2 row.  After every segment but the last it writes the state so
+// far, the exclusive prefix of the next segment, as fp16 with one exponent per (segment,
+// work-group).
 // Kernel 2 (gout_kernel): one work-group per 256 queries (four waves of 64).  The inter-segment
 // part is O^T += T^T Phi(Q)^T over all groups on fp16 MFMAs: T^T blocks of 8 groups copied into
 // LDS (buffer_load ... lds, double-buffered), Phi(Q) formed in registers from the query's
@@ -35,59 +26,12 @@
 
 #include "../../include/based_la.h"
 #include "la_common.hpp"
+#include "la_general.hpp"
 #include "la_internal.hpp"
 #include "la_stage.hpp"
 
 namespace la {
 namespace {
-
-constexpr int GL = 512;    // tokens per segment
-constexpr int GC = 64;     // tokens per chunk of the state kernel
-constexpr int GQ = 256;    // queries per output work-group
-
-template <int DP>
-struct GFeat {
-  static constexpr int DB = DP / 16;
-  static constexpr int NQ = 8 * DB * (DB + 1);      // quad groups
-  static constexpr int NG = NQ + DB + 1;            // + linear + constant
-  static constexpr int NGP = (NG + 1) & ~1;         // even: two groups per 32-feature tile
-  static constexpr int NT = NGP / 2;                // tiles
-  static constexpr int NGB = (NGP + 7) / 8;         // blocks of 8 groups (128 features)
-  static constexpr int NWGA = (NGP + 15) / 16;      // state work-groups per head
-};
-
-// (i, J) of group g in the i-major order above; the padding group past NG repeats the constant
-// group (the output kernel never reads it).
-template <int DP>
-__device__ __forceinline__ void group_ij(int g, int& i, int& J) {
-  constexpr int DB = DP / 16, NQ = GFeat<DP>::NQ;
-  if (g < NQ) {
-    int start = 0;
-#pragma unroll
-    for (int I = 0; I < DB; ++I) {
-      const int c = DB - I, cnt = 16 * c;
-      if (g < start + cnt) {
-        const int off = g - start;
-        i = 16 * I + off / c;
-        J = I + off % c;
-        return;
-      }
-      start += cnt;
-    }
-  }
-  const int r = g - NQ;
-  i = DP;
-  J = r < DB ? r : DB;
-}
-
-template <int DP>
-__device__ __forceinline__ float group_weight(int g) {
-  if (g >= GFeat<DP>::NG) return 0.f;
-  int i, J;
-  group_ij<DP>(g, i, J);
-  if (i < DP) return J == (i >> 4) ? 0.5f : 1.0f;
-  return 1.0f;
-}
 
 struct GParams {
   const uint16_t* q;
@@ -777,10 +721,14 @@ int launch_dp(const GParams& p, int DVT, hipStream_t stream) {
 
 }  // namespace
 
-bool general_chunked_shape(int d, int dv, bool in_f32) { return !in_f32 && d >= 1 && d <= 64 && dv >= 1 && dv <= 128; }
+bool general_chunked_shape(int d, int dv, bool in_f32) {
+  (void)in_f32;
+  return d >= 1 && d <= 64 && dv >= 1 && dv <= 128;
+}
 
 size_t general_chunked_bytes(int BH, int N, int d, int dv, bool in_f32) {
   if (!general_chunked_shape(d, dv, in_f32)) return (size_t)-1;
+  if (in_f32) return general_chunked_f32_bytes(BH, N, d, dv);
   const int nseg = (N + GL - 1) / GL;
   if (nseg <= 1) return 0;
   return glayout(BH, N, d, dv).total;
@@ -788,6 +736,7 @@ size_t general_chunked_bytes(int BH, int N, int d, int dv, bool in_f32) {
 
 int launch_general_chunked(const ChunkedArgs& a, hipStream_t stream) {
   if (!general_chunked_shape(a.d, a.dv, a.in_f32)) return LA_ERR_UNSUPPORTED_DIM;
+  if (a.in_f32) return launch_general_chunked_f32(a, stream);
   const int DP = dp_of(a.d), DVT = dvt_of(a.dv);
   GParams p{};
   p.q = static_cast<const uint16_t*>(a.q);

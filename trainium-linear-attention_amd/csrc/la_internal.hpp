@@ -110,10 +110,13 @@ int chunked_chunk_tokens();   // tokens per chunk of the chunked kernels
 // segment and there is no initial state, (size_t)-1 for unsupported shapes.
 size_t chunked_scratch_bytes(int BH, int N, int d, int dv, bool with_state, bool in_f32);
 int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream);
-// Chunked path for the other head dims (d <= 64, dv <= 128, bf16): segment states + outputs.
+// Segment-state chunked path for the shapes the recurrence kernel does not take (d <= 64,
+// dv <= 128; bf16 in chunked_general.hip, fp32 in chunked_general_f32.hip).
 bool general_chunked_shape(int d, int dv, bool in_f32);
 size_t general_chunked_bytes(int BH, int N, int d, int dv, bool in_f32);   // workspace, (size_t)-1 if unsupported
 int launch_general_chunked(const ChunkedArgs& a, hipStream_t stream);
+size_t general_chunked_f32_bytes(int BH, int N, int d, int dv);
+int launch_general_chunked_f32(const ChunkedArgs& a, hipStream_t stream);
 bool layer_fused_shape(int d, int dv, int dsw, int window);   // shapes of chunked_layer_kernel
 int launch_based_layer(const LayerArgs& a, hipStream_t stream);
 int launch_feature_map(const FeatureMapArgs& a, hipStream_t stream);

@@ -40,6 +40,7 @@ _SIGNATURES = {
                                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int,
                                               _c_void, _c_size, _c_void]),
     "la_based_chunked_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "la_based_chunked_workspace_bytes_dt": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "la_based_chunked_chunk_used": (_c_int, [_c_int]),
     "la_based_chunked_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
                                       _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int, _c_void,
@@ -68,7 +69,7 @@ _SIGNATURES = {
     "la_taylor_feature_map": (_c_int, [_c_void, _c_int, _c_void, _c_int, ctypes.c_longlong, _c_int, _c_void]),
 }
 
-EXPECTED_ABI = 8
+EXPECTED_ABI = 9
 
 
 class BasedLAError(RuntimeError):

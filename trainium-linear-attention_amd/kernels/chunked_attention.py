@@ -14,9 +14,10 @@ state stays on chip across chunks (the NKI kernel round-trips it through HBM,
 kernels/nki_attention_chunked.py:92-102).  dv may differ from d.
 
 Two chunked paths: the recurrence kernel for bf16 inputs with d = 16 and dv <= 64 (the BASED
-configuration), and for other head dims (d <= 64, dv <= 128, bf16) a segment-state path (state
-prefixes of 512-token segments in the feature basis, then every query's contraction with its
-segment's prefix plus the quadratic form inside the segment).  Both are linear in the sequence
+configuration), and for other head dims and fp32 inputs (d <= 64, dv <= 128) a segment-state
+path (state prefixes of 512-token segments in the feature basis, then every query's contraction
+with its segment's prefix plus the quadratic form inside the segment; fp32 throughout for fp32
+inputs).  Both are linear in the sequence
 length.  Shapes outside both are computed by the fused parallel kernel, which evaluates the same
 function (numerator or normalised) on the GPU.  ``chunk_size`` is the reference's argument
 (any value >= 1); the kernel's recurrence runs 128-token chunks (``la_based_chunked_chunk_used``
@@ -63,8 +64,8 @@ def chunked_supported(d: int, dv: int, dtype: torch.dtype) -> bool:
 
 
 def general_chunked_supported(d: int, dv: int, dtype: torch.dtype) -> bool:
-    """Shapes of the segment-state chunked path (bf16, d <= 64, dv <= 128), linear in N."""
-    return 1 <= d <= 64 and 1 <= dv <= 128 and dtype == torch.bfloat16
+    """Shapes of the segment-state chunked path (bf16 or fp32, d <= 64, dv <= 128), linear in N."""
+    return 1 <= d <= 64 and 1 <= dv <= 128 and dtype in (torch.bfloat16, torch.float32)
 
 
 def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, out_dtype=None,
@@ -96,7 +97,7 @@ def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, 
     qc, kc, vc = (_as_kernel_input(x, cdt) for x in (q, k, v))
     out = torch.empty(b, h, t, dv, dtype=kdt, device=q.device)
     L = _lib.lib()
-    ws_bytes = int(L.la_based_chunked_workspace_bytes(b, h, t, d, dv, int(chunk_size)))
+    ws_bytes = int(L.la_based_chunked_workspace_bytes_dt(b, h, t, d, dv, int(chunk_size), _lib.dtype_code(cdt)))
     if ws_bytes == (1 << 64) - 1:
         raise _lib.BasedLAError(f"chunked kernel does not support d={d}, dv={dv}, chunk={chunk_size}")
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)

@@ -123,9 +123,9 @@ def ref_based_attn(q, k, v, eps=1e-6):
 CHUNKED_MIN_T = 256
 
 # Sequence length from which ``solution`` uses the segment-state chunked path for the other head
-# dims (d <= 64, dv <= 128, bf16).  Measured on MI355X at B2 H16 d64 dv64 bf16: 0.513 ms against
-# 0.444 ms for the fused kernel at N = 8192, 3.2 ms at B1 H16 N = 65536, where the fused kernel's
-# quadratic work is 32 times that at N = 8192 for half the heads.
+# dims and for fp32 inputs (d <= 64, dv <= 128).  Measured on MI355X at N = 8192, B2 H16: bf16 d64
+# dv64 0.513 ms against 0.444 ms for the fused kernel, fp32 d16 dv64 1.21 against 1.45 ms, fp32
+# d64 2.48 against 2.29 ms; the fused kernel's work grows with N^2, the chunked paths' with N.
 GENERAL_CHUNKED_MIN_T = 16384
 
 
@@ -134,8 +134,8 @@ def solution(q, k, v, eps=1e-6):
 
     Dispatches by sequence length between the parallel fused kernel and the chunked kernels,
     which compute the same function: the d = 16 recurrence kernel from ``CHUNKED_MIN_T`` tokens,
-    the segment-state path for other head dims from ``GENERAL_CHUNKED_MIN_T``; fp32 inputs and
-    other shapes go to the fused kernel.  There is no PyTorch fallback.
+    the segment-state path for other head dims and fp32 inputs from ``GENERAL_CHUNKED_MIN_T``;
+    shorter sequences and other shapes go to the fused kernel.  There is no PyTorch fallback.
     """
     from .chunked_attention import chunked_based_attn, chunked_supported, general_chunked_supported
     t, d, dv = q.shape[-2], q.shape[-1], v.shape[-1]
