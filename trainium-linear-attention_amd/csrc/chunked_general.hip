@@ -15,8 +15,8 @@
 // far, the exclusive prefix of the next segment, as fp16 with one exponent per (segment,
 // work-group).
 // Kernel 2 (gout_kernel): one work-group per 256 queries (four waves of 64).  The inter-segment
-// part is O^T += T^T Phi(Q)^T over all groups on fp16 MFMAs: T^T blocks of 8 groups copied into
-// LDS (buffer_load ... lds, double-buffered), Phi(Q) formed in registers from the query's
+// part is O^T += T^T Phi(Q)^T over all groups on fp16 MFMAs: T^T blocks of 4 groups copied into
+// LDS (buffer_load ... lds, three blocks in flight), Phi(Q) formed in registers from the query's
 // features a'/m (m a power of two >= max |a'|, so every feature lies in [-1, 1]) with one
 // v_pk_mul_f16 per two features; the per-group weight times 2^(E_tile - E_max) goes on a'_i.
 // The denominator takes the same features against z with v_dot2.  The intra-segment part is the
@@ -38,8 +38,8 @@ struct GParams {
   const uint16_t* k;
   const uint16_t* v;
   void* out;
-  uint16_t* T;      // [seg-1][BH][NGB][DVP rows][128] fp16, 16-byte units of a row XOR (row & 15)
-  uint16_t* Z;      // [seg-1][BH][NGB * 128] fp16
+  uint16_t* T;      // [seg-1][BH][NGB][DVP rows][64] fp16, 16-byte unit u of a row at u ^ ((row >> 1) & 7)
+  uint16_t* Z;      // [seg-1][BH][NGB * 64] fp16
   int* E;           // [seg-1][BH][NWGA]
   uint16_t* KV;     // converted chunks [BH][chunks before the last segment][GChunk rows][64]
   u32x2* CE;        // their exponents {Ec, Ez}
@@ -49,12 +49,6 @@ struct GParams {
 };
 
 constexpr u32 kOnesBf16 = 0x3f803f80u;
-
-__device__ __forceinline__ void sync_copies() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
-  asm volatile("" ::: "memory");
-}
 
 // Wait until at most n of this wave's vector-memory operations are outstanding (s_waitcnt
 // vmcnt(n), n <= 31; lgkmcnt and expcnt untouched).
@@ -366,8 +360,8 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
       const int E = max(max(ea, ez) - 13, -100);
       const float sc = __builtin_ldexpf(1.0f, eref - E), scz = __builtin_ldexpf(1.0f, ezref - E);
       const size_t slot = (size_t)s * p.BH + bh;
-      uint16_t* Ts = p.T + slot * (size_t)(FT::NGB * DVP * 128);
-      uint16_t* Zs = p.Z + slot * (size_t)(FT::NGB * 128);
+      uint16_t* Ts = p.T + slot * (size_t)(FT::NGB * DVP * 64);
+      uint16_t* Zs = p.Z + slot * (size_t)(FT::NGB * 64);
 #pragma unroll
       for (int mw = 0; mw < 2; ++mw) {
         if (!tv[mw]) continue;
@@ -378,8 +372,8 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
             const int f0 = 32 * tt + 8 * q4 + 4 * h;
-            const int gb = f0 >> 7, uu = (f0 & 127) >> 3;
-            const size_t off = (size_t)gb * (DVP * 128) + row * 128 + ((uu ^ (row & 15)) << 3) + (f0 & 7);
+            const int gb = f0 >> 6, uu = (f0 & 63) >> 3;
+            const size_t off = (size_t)gb * (DVP * 64) + row * 64 + gswz(row, uu) + (f0 & 7);
             const f32x16& a = acc[mw][nt];
             *reinterpret_cast<u32x2*>(Ts + off) =
                 (u32x2){pack_f16x2(a[4 * q4] * sc, a[4 * q4 + 1] * sc), pack_f16x2(a[4 * q4 + 2] * sc, a[4 * q4 + 3] * sc)};
@@ -401,11 +395,13 @@ __global__ __launch_bounds__(256, DVT == 4 ? 1 : 2) void gout_kernel(const GPara
   constexpr int DB = DP / 16, DVP = 32 * DVT, KS = DP / 16;
   constexpr int NR = DP / 2 + 4;                 // rotated fp16 pairs of a'/m per token tile
   constexpr int NU = DP / 2 + 8;                 // unrotated pairs (a' through index DP + 15)
-  constexpr int TB = DVP * 128 + 512;            // halves per T stage: block, then 1 KB of z
+  constexpr int TB = DVP * 64 + 512;             // halves per T stage: block, then 1 KB of z
+  constexpr int NS = 4;                          // T stages (blocks in flight: NS - 1)
+  constexpr int NB = (FT::NG + 3) / 4;           // blocks holding groups the loop reads
   using Stager = BlockStager<KS, DVT, VEC, false>;
   constexpr int KROW = Stager::KROW;
   constexpr int IB = 2 * (BN * KROW + DVP * VROW);
-  constexpr int BIG = 2 * TB > IB ? 2 * TB : IB;
+  constexpr int BIG = NS * TB > IB ? NS * TB : IB;
   __shared__ __attribute__((aligned(16))) uint16_t Aq[(DP + 1) * GQ];
   __shared__ __attribute__((aligned(16))) uint16_t big[BIG];
   __shared__ float wtab[FT::NGP];
@@ -491,19 +487,21 @@ __global__ __launch_bounds__(256, DVT == 4 ? 1 : 2) void gout_kernel(const GPara
     for (int x = 0; x < FT::NWGA; ++x) emax = max(emax, Es[x]);
     for (int g = tid; g < FT::NGP; g += 256)
       wtab[g] = group_weight<DP>(g) * __builtin_ldexpf(1.0f, Es[g >> 4] - emax);
-    const u32x4 rT = buffer_rsrc(p.T + slot * (size_t)(FT::NGB * DVP * 128), (u32)(FT::NGB * DVP * 256));
-    const u32x4 rZ = buffer_rsrc(p.Z + slot * (size_t)(FT::NGB * 128), (u32)(FT::NGB * 256));
-    constexpr int UT = DVP / 4;   // 1 KB units of a T block
+    const u32x4 rT = buffer_rsrc(p.T + slot * (size_t)(FT::NGB * DVP * 64), (u32)(FT::NGB * DVP * 128));
+    const u32x4 rZ = buffer_rsrc(p.Z + slot * (size_t)(FT::NGB * 64), (u32)(FT::NGB * 128));
+    constexpr int UT = DVP / 8;   // 1 KB units of a T block, then one of z
+    const int my_units = (UT + 1) / 4 + (w < (UT + 1) % 4 ? 1 : 0);
     auto issue = [&](int gb) {
-      const u32 base = lds_addr(&big[(gb & 1) * TB]);
+      if (gb >= NB) return;
+      const u32 base = lds_addr(&big[(gb % NS) * TB]);
       for (int u = w; u <= UT; u += 4) {
         if (u < UT)
-          lds_copy16(rT, base + 1024 * u, gb * (DVP * 256) + 1024 * u + 16 * lane);
+          lds_copy16(rT, base + 1024 * u, gb * (DVP * 128) + 1024 * u + 16 * lane);
         else
-          lds_copy16(rZ, base + DVP * 256, gb * 256 + 16 * lane);
+          lds_copy16(rZ, base + DVP * 128, gb * 128 + 16 * lane);
       }
     };
-    issue(0);
+    for (int b = 0; b < NS - 1; ++b) issue(b);
     int g = 0;
     for (int i = 0; i <= DP; ++i) {
       float ai[2];
@@ -514,21 +512,24 @@ __global__ __launch_bounds__(256, DVT == 4 ? 1 : 2) void gout_kernel(const GPara
 #pragma unroll
       for (int J = 0; J <= DB; ++J) {
         if (J < js || J > je) continue;
-        if ((g & 7) == 0) {
-          sync_copies();
+        if ((g & 3) == 0) {
+          // this wave's copies of block g / 4 landed, then every wave's; every wave is also done
+          // with the block before, whose stage the next copy reuses
+          const int b = g >> 2;
+          wait_vm(my_units * min(NS - 2, NB - 1 - b));
           __syncthreads();
-          if ((g >> 3) + 1 < FT::NGB) issue((g >> 3) + 1);
+          issue(b + NS - 1);
         }
-        const uint16_t* st = &big[((g >> 3) & 1) * TB];
-        const int sl = g & 7;
+        const uint16_t* st = &big[((g >> 2) % NS) * TB];
+        const int sl = g & 3;
         const float wg = wtab[g];
         u32x4 tf[DVT];
 #pragma unroll
         for (int mt = 0; mt < DVT; ++mt) {
           const int row = 32 * mt + n;
-          tf[mt] = *reinterpret_cast<const u32x4*>(st + row * 128 + (((2 * sl + h) ^ (row & 15)) << 3));
+          tf[mt] = *reinterpret_cast<const u32x4*>(st + row * 64 + gswz(row, 2 * sl + h));
         }
-        const u32x4 zr = *reinterpret_cast<const u32x4*>(st + DVP * 128 + 16 * sl + 8 * h);
+        const u32x4 zr = *reinterpret_cast<const u32x4*>(st + DVP * 64 + 16 * sl + 8 * h);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           const float a = ai[nt] * wg;
@@ -589,13 +590,21 @@ __global__ __launch_bounds__(256, DVT == 4 ? 1 : 2) void gout_kernel(const GPara
         for (int kk = 0; kk < KS; ++kk) sc = mfma32x32x16(kf[kk], qf[nt][kk], sc);
         const int tok = tb + n;
         float pv[16];
+        // tiles wholly below the diagonal and inside the sequence need no mask
+        const bool masked = kb2 + 31 > tb || kb2 + 31 >= N;
+        if (masked) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float x = sc[r] * p.scale;
-          float pr = 1.0f + x + 0.5f * x * x;
-          const int key = kb2 + c32_row(r, h);
-          if (key > tok || key >= N) pr = 0.f;
-          pv[r] = pr;
+          for (int r = 0; r < 16; ++r) {
+            const float x = sc[r] * p.scale;
+            const int key = kb2 + c32_row(r, h);
+            pv[r] = (key > tok || key >= N) ? 0.f : __builtin_fmaf(x, __builtin_fmaf(0.5f, x, 1.0f), 1.0f);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float x = sc[r] * p.scale;
+            pv[r] = __builtin_fmaf(x, __builtin_fmaf(0.5f, x, 1.0f), 1.0f);
+          }
         }
         // p as bf16 hi + lo (16 significant bits; V is exact in bf16), and the row sums from the
         // same two parts, so that the rounding of a row cancels in the quotient
@@ -672,8 +681,8 @@ GLayout glayout_dp(int BH, int nseg, int DVT) {
   const auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
   GLayout L{};
   L.t = 0;
-  L.z = L.t + up(nslot * FT::NGB * 128 * (32 * DVT) * 2);
-  L.e = L.z + up(nslot * FT::NGB * 128 * 2);
+  L.z = L.t + up(nslot * FT::NGB * 64 * (32 * DVT) * 2);
+  L.e = L.z + up(nslot * FT::NGB * 64 * 2);
   L.kv = L.e + up(nslot * FT::NWGA * 4);
   L.ce = L.kv + up(nchk * halves * 2);
   L.total = L.ce + up(nchk * 8);

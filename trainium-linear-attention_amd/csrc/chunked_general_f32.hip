@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void g32_state_kernel(const G32Params p) {
 
 // ---------------------------------------------------------------- kernel 2: outputs
 template <int DP, int DVT>
-__global__ __launch_bounds__(256, 2) void g32_out_kernel(const G32Params p) {
+__global__ __launch_bounds__(256, DVT == 4 ? 1 : 2) void g32_out_kernel(const G32Params p) {
   using FT = GFeat<DP>;
   constexpr int DB = DP / 16, DVP = 32 * DVT;
   constexpr int NR = DP + 16;                    // a'/m of the query, lane half 1 one further on

@@ -31,7 +31,7 @@ struct GFeat {
   static constexpr int NG = NQ + DB + 1;            // + linear + constant
   static constexpr int NGP = (NG + 1) & ~1;         // even: two groups per 32-feature tile
   static constexpr int NT = NGP / 2;                // tiles
-  static constexpr int NGB = (NGP + 7) / 8;         // blocks of 8 groups (128 features)
+  static constexpr int NGB = (NGP + 3) / 4;         // blocks of 4 groups (64 features)
   static constexpr int NWGA = (NGP + 15) / 16;      // state work-groups per head
 };
 
