@@ -78,6 +78,8 @@ def parse():
     ap.add_argument("--clock-transient", action="store_true",
                     help="only time single calls of the headline attention kernel: 60 back to back from idle, then 20 "
                          "after 20 ms idle gaps (the step from idle to load that --settle-ms waits out)")
+    ap.add_argument("--general", action="store_true",
+                    help="time the segment-state chunked path (d != 16, fp32) beside the fused kernel")
     ap.add_argument("--crossover", action="store_true",
                     help="only sweep sequence lengths: whole parallel forward vs chunked forward (d=16, dv=64, bf16), "
                          "the measurement behind solution()'s dispatch threshold")
@@ -313,6 +315,38 @@ def crossover(steps, warmup, rotate, device):
                 best = None
         first[f"B{B}H{H}"] = best
     return {"crossover": rows, "chunked_faster_from": first}
+
+
+# shapes of the segment-state chunked path (head dims other than 16, fp32 inputs):
+# (B, H, N, d, dv, dtype); the fused kernel is timed beside it up to N = 8192
+GENERAL_SHAPES = [(2, 16, 8192, 64, 64, "bf16"), (1, 16, 65536, 64, 64, "bf16"), (2, 16, 8192, 32, 128, "bf16"),
+                  (2, 16, 8192, 16, 64, "f32"), (1, 16, 65536, 16, 64, "f32")]
+GENERAL_SEGMENT = 512   # tokens per segment: the span of the path's quadratic part
+
+
+def general_bench(steps, warmup, device):
+    """ms per call of la_based_chunked_fwd on the segment-state path and of the fused parallel
+    kernel (N <= 8192) on the same inputs; TFLOP/s with the chunked FLOP count of the benchmark
+    configurations, F = 1 + d + d^2 and the segment as the quadratic span."""
+    rows = []
+    for B, H, N, d, dv, dt in GENERAL_SHAPES:
+        q, k, v = make_inputs(B, H, N, d, dv, dt, 21, True, device)
+        esz = 2 if dt == "bf16" else 4
+        flop, _ = work("chunked", B, H, N, d, dv, esz, GENERAL_SEGMENT, 64)
+        row = {"B": B, "H": H, "N": N, "d": d, "dv": dv, "dtype": dt}
+        ms = time_calls([Call("chunked", q, k, v, 64, 64)], steps, warmup)
+        row["chunked_ms"] = round(ms, 5)
+        row["chunked_tflops"] = round(flop / (ms * 1e-3) / 1e12, 2)
+        if N <= 8192:
+            pflop, _ = work("parallel", B, H, N, d, dv, esz, 64, 64)
+            pms = time_calls([Call("parallel", q, k, v, 64, 64)], steps, warmup)
+            row["parallel_ms"] = round(pms, 5)
+            row["parallel_tflops"] = round(pflop / (pms * 1e-3) / 1e12, 2)
+        rows.append(row)
+        print(json.dumps(row), file=sys.stderr, flush=True)
+        del q, k, v
+        torch_empty_cache()
+    return {"general": rows}
 
 
 # full BASED layer shapes: (B, H, N, d of the linear branch, d_sw of the softmax branch, dv, window)
@@ -558,6 +592,10 @@ def main():
 
     if args.crossover:
         print(json.dumps(crossover(args.steps, args.warmup, args.rotate, device)))
+        return
+
+    if args.general:
+        print(json.dumps(general_bench(args.steps, args.warmup, device)))
         return
 
     if args.clock_transient:

@@ -43,6 +43,8 @@ struct GParams {
   int* E;           // [seg-1][BH][NWGA]
   uint16_t* KV;     // converted chunks [BH][chunks before the last segment][GChunk rows][64]
   u32x2* CE;        // their exponents {Ec, Ez}
+  float* Tot;       // per (part < nparts - 1, head, state work-group, thread): its part's sums
+  int nparts, spp;  // the state sweep split into parts of spp segments
   int BH, N, d, dv, nseg, vec;
   float scale, eps;
   int normalize, out_f32;
@@ -188,7 +190,10 @@ __global__ __launch_bounds__(256) void gprep_kernel(const GParams p) {
 }
 
 // ---------------------------------------------------------------- kernel 1: segment states
-template <int DP, int DVT>
+// Sequences with few heads split the sweep into p.nparts parts of p.spp segments: a TOTAL pass
+// sums every part but the last (no prefixes written), then each part's work-group starts from
+// the totals of the parts before it and writes its segments' prefixes.
+template <int DP, int DVT, bool TOTAL>
 __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
   using FT = GFeat<DP>;
   using CK = GChunk<DP, DVT>;
@@ -200,9 +205,11 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
   const int nwga = FT::NWGA;
+  const int units = p.BH * nwga;
+  const int part = blockIdx.x / units;
   int bh, wga;
   {
-    const int id = blockIdx.x;
+    const int id = blockIdx.x - part * units;
     if ((p.BH & 7) == 0) {
       const int x = id & 7, r = id >> 3, hg = r / nwga;
       wga = r - hg * nwga;
@@ -213,6 +220,9 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
     }
   }
   const int nch = (p.nseg - 1) * (GL / GC);
+  const int cps = GL / GC;
+  const int c0 = part * p.spp * cps, c1 = min((part + 1) * p.spp, p.nseg - 1) * cps;   // this part's chunks
+  constexpr int PER = 2 * DVT * 16 + 2;   // a thread's sums: accumulators, then z partials
   const uint16_t* __restrict__ src = p.KV + (size_t)bh * nch * CK::HALVES;
   const u32x2* __restrict__ ce = p.CE + (size_t)bh * nch;
 
@@ -256,7 +266,7 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
   const int my_units = CK::UNITS / 4 + (w < CK::UNITS % 4 ? 1 : 0);
   const u32x4 rsrc = buffer_rsrc(src, (u32)((size_t)nch * CK::HALVES * 2));
   auto issue = [&](int c) {
-    if (c >= nch) return;
+    if (c >= c1) return;
     const u32 base = lds_addr(&ring[c % NS][0]);
 #pragma unroll
     for (int x = 0; x < UW; ++x) {
@@ -275,12 +285,25 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
 #pragma unroll
     for (int nt = 0; nt < DVT; ++nt) acc[mw][nt] = splat16(0.f);
 
-  for (int c = 0; c < NS - 1; ++c) issue(c);
-  const int cps = GL / GC;
-  for (int gc = 0; gc < nch; ++gc) {
+  if (!TOTAL) {
+    // the parts before this one
+    for (int q = 0; q < part; ++q) {
+      const float* t = p.Tot + (((size_t)q * p.BH + bh) * nwga + wga) * (256 * PER) + tid * PER;
+#pragma unroll
+      for (int mw = 0; mw < 2; ++mw)
+#pragma unroll
+        for (int nt = 0; nt < DVT; ++nt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[mw][nt][r] += t[(mw * DVT + nt) * 16 + r];
+      zc[0] += t[PER - 2];
+      zc[1] += t[PER - 1];
+    }
+  }
+  for (int c = c0; c < c0 + NS - 1; ++c) issue(c);
+  for (int gc = c0; gc < c1; ++gc) {
     // this wave's copies of chunk gc landed (later chunks may still be in flight), then every
     // wave's; every wave is also done with chunk gc - 1, whose stage the next copy reuses
-    wait_vm(my_units * min(NS - 2, nch - 1 - gc));
+    wait_vm(my_units * min(NS - 2, c1 - 1 - gc));
     __syncthreads();
     issue(gc + NS - 1);
     const uint16_t* st = &ring[gc % NS][0];
@@ -329,7 +352,7 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
       for (int ks = 0; ks < GC / 16; ++ks) kstep(ks, false);
     }
 
-    if ((gc + 1) % cps == 0) {
+    if (!TOTAL && (gc + 1) % cps == 0) {
       // end of segment s = gc / cps: write the prefix of segment s + 1 (slot s).  acc holds
       // T 2^-eref, zc z 2^-ezref; the slot's exponent E puts the largest of both in
       // [2^13, 2^14).
@@ -385,6 +408,17 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
       // the stores out before the copy waits above count this wave's copies again
       wait_vm(0);
     }
+  }
+  if (TOTAL) {
+    float* t = p.Tot + (((size_t)part * p.BH + bh) * nwga + wga) * (256 * PER) + tid * PER;
+#pragma unroll
+    for (int mw = 0; mw < 2; ++mw)
+#pragma unroll
+      for (int nt = 0; nt < DVT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) t[(mw * DVT + nt) * 16 + r] = acc[mw][nt][r];
+    t[PER - 2] = zc[0];
+    t[PER - 1] = zc[1];
   }
 }
 
@@ -661,10 +695,23 @@ __global__ __launch_bounds__(256, DVT == 4 ? 1 : 2) void gout_kernel(const GPara
 int dp_of(int d) { return 16 * ((d + 15) / 16); }
 int dvt_of(int dv) { return dv <= 32 ? 1 : dv <= 64 ? 2 : 4; }
 
+// Parts of the state sweep: when the (head, work-group) pairs fill less than half of 256 CUs,
+// enough parts for two work-groups per CU (the totals pass sweeps all but the last part a second
+// time, which pays only then), at least two segments per part.
+void state_parts(int BH, int nwga, int nseg, int& nparts, int& spp) {
+  const int units = BH * nwga;
+  const int want = units < 128 ? (512 + units - 1) / units : 1;
+  nparts = max(1, min(want, (nseg - 1) / 2));
+  spp = (nseg - 1 + nparts - 1) / nparts;
+  nparts = (nseg - 1 + spp - 1) / spp;
+}
+
 // Workspace regions of one call: per (segment slot, head) the T blocks, z and the exponents; per
-// (head, chunk before the last segment) the converted chunk and its two exponents.
+// (head, chunk before the last segment) the converted chunk and its two exponents; the part
+// totals of the state sweep.
 struct GLayout {
-  size_t t, z, e, kv, ce, total;
+  size_t t, z, e, kv, ce, tot, total;
+  int nparts, spp;
 };
 
 template <int DP>
@@ -685,7 +732,9 @@ GLayout glayout_dp(int BH, int nseg, int DVT) {
   L.e = L.z + up(nslot * FT::NGB * 64 * 2);
   L.kv = L.e + up(nslot * FT::NWGA * 4);
   L.ce = L.kv + up(nchk * halves * 2);
-  L.total = L.ce + up(nchk * 8);
+  L.tot = L.ce + up(nchk * 8);
+  state_parts(BH, FT::NWGA, nseg, L.nparts, L.spp);
+  L.total = L.tot + up((size_t)(L.nparts - 1) * BH * FT::NWGA * 256 * (2 * DVT * 16 + 2) * 4);
   return L;
 }
 
@@ -707,7 +756,14 @@ int launch_g(const GParams& p, hipStream_t stream) {
     hipLaunchKernelGGL((gprep_kernel<DP, DVT>), dim3((unsigned)(p.BH * nch)), dim3(256), 0, stream, p);
     int e = (int)hipGetLastError();
     if (e != 0) return e;
-    hipLaunchKernelGGL((gstate_kernel<DP, DVT>), dim3((unsigned)(p.BH * FT::NWGA)), dim3(256), 0, stream, p);
+    const unsigned units = (unsigned)(p.BH * FT::NWGA);
+    if (p.nparts > 1) {
+      hipLaunchKernelGGL((gstate_kernel<DP, DVT, true>), dim3(units * (unsigned)(p.nparts - 1)), dim3(256), 0, stream,
+                         p);
+      e = (int)hipGetLastError();
+      if (e != 0) return e;
+    }
+    hipLaunchKernelGGL((gstate_kernel<DP, DVT, false>), dim3(units * (unsigned)p.nparts), dim3(256), 0, stream, p);
     e = (int)hipGetLastError();
     if (e != 0) return e;
   }
@@ -778,6 +834,9 @@ int launch_general_chunked(const ChunkedArgs& a, hipStream_t stream) {
     p.E = reinterpret_cast<int*>(ws + L.e);
     p.KV = reinterpret_cast<uint16_t*>(ws + L.kv);
     p.CE = reinterpret_cast<u32x2*>(ws + L.ce);
+    p.Tot = reinterpret_cast<float*>(ws + L.tot);
+    p.nparts = L.nparts;
+    p.spp = L.spp;
   }
   switch (DP) {
     case 16: return launch_dp<16>(p, DVT, stream);

@@ -32,6 +32,8 @@ struct G32Params {
   void* out;
   float* T;      // [seg-1][BH][F][DVP]
   float* Z;      // [seg-1][BH][F]
+  float* Tot;    // per (part < nparts - 1, head, state work-group, thread): its part's sums
+  int nparts, spp;
   int BH, N, d, dv, nseg;
   float scale, eps;
   int normalize, out_f32;
@@ -56,7 +58,9 @@ __device__ __forceinline__ void wait_vm32(int n) {
 }
 
 // ---------------------------------------------------------------- kernel 1: segment states
-template <int DP, int DVT>
+// Sequences with few heads split the sweep into p.nparts parts of p.spp segments: a TOTAL pass
+// sums every part but the last, then each part's work-group starts from the totals before it.
+template <int DP, int DVT, bool TOTAL>
 __global__ __launch_bounds__(256) void g32_state_kernel(const G32Params p) {
   using FT = GFeat<DP>;
   constexpr int DVP = 32 * DVT, NS = 4;
@@ -66,9 +70,11 @@ __global__ __launch_bounds__(256) void g32_state_kernel(const G32Params p) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
   const int nwga = FT::NWGA;
+  const int units = p.BH * nwga;
+  const int part = blockIdx.x / units;
   int bh, wga;
   {
-    const int id = blockIdx.x;
+    const int id = blockIdx.x - part * units;
     if ((p.BH & 7) == 0) {
       const int x = id & 7, r = id >> 3, hg = r / nwga;
       wga = r - hg * nwga;
@@ -110,12 +116,14 @@ __global__ __launch_bounds__(256) void g32_state_kernel(const G32Params p) {
     sv[nt] = col < dv ? dv : 0;
   }
 
-  const int nch = (p.nseg - 1) * (GL / GC32);
+  const int cps = GL / GC32;
+  const int c0 = part * p.spp * cps, c1 = min((part + 1) * p.spp, p.nseg - 1) * cps;   // this part's chunks
+  constexpr int PER = 2 * DVT * 16 + 2;   // a thread's sums: accumulators, then z partials
   const u32x4 rk = buffer_rsrc(p.k + (size_t)bh * N * d, (u32)((size_t)N * d * 4));
   const u32x4 rv = buffer_rsrc(p.v + (size_t)bh * N * dv, (u32)((size_t)N * dv * 4));
   const int my_units = (ku + vu) / 4 + (w < (ku + vu) % 4 ? 1 : 0);
   auto issue = [&](int c) {
-    if (c >= nch) return;
+    if (c >= c1) return;
     const u32 base = lds_addr(&ring[c % NS][0]);
     for (int u = w; u < ku + vu; u += 4) {
       if (u < ku)
@@ -132,11 +140,24 @@ __global__ __launch_bounds__(256) void g32_state_kernel(const G32Params p) {
 #pragma unroll
     for (int nt = 0; nt < DVT; ++nt) acc[mw][nt] = splat16(0.f);
 
+  if (!TOTAL) {
+    // the parts before this one
+    for (int q = 0; q < part; ++q) {
+      const float* t = p.Tot + (((size_t)q * p.BH + bh) * nwga + wga) * (256 * PER) + tid * PER;
+#pragma unroll
+      for (int mw = 0; mw < 2; ++mw)
+#pragma unroll
+        for (int nt = 0; nt < DVT; ++nt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[mw][nt][r] += t[(mw * DVT + nt) * 16 + r];
+      zc[0] += t[PER - 2];
+      zc[1] += t[PER - 1];
+    }
+  }
   __syncthreads();
-  for (int c = 0; c < NS - 1; ++c) issue(c);
-  const int cps = GL / GC32;
-  for (int gc = 0; gc < nch; ++gc) {
-    wait_vm32(my_units * min(NS - 2, nch - 1 - gc));
+  for (int c = c0; c < c0 + NS - 1; ++c) issue(c);
+  for (int gc = c0; gc < c1; ++gc) {
+    wait_vm32(my_units * min(NS - 2, c1 - 1 - gc));
     __syncthreads();
     issue(gc + NS - 1);
     const float* st = &ring[gc % NS][0];
@@ -155,7 +176,7 @@ __global__ __launch_bounds__(256) void g32_state_kernel(const G32Params p) {
       }
     }
 
-    if ((gc + 1) % cps == 0) {
+    if (!TOTAL && (gc + 1) % cps == 0) {
       const int s = gc / cps;
       const size_t slot = (size_t)s * p.BH + bh;
       constexpr int F = 16 * FT::NGP;
@@ -175,6 +196,17 @@ __global__ __launch_bounds__(256) void g32_state_kernel(const G32Params p) {
       // the stores out before the copy waits above count this wave's copies again
       wait_vm32(0);
     }
+  }
+  if (TOTAL) {
+    float* t = p.Tot + (((size_t)part * p.BH + bh) * nwga + wga) * (256 * PER) + tid * PER;
+#pragma unroll
+    for (int mw = 0; mw < 2; ++mw)
+#pragma unroll
+      for (int nt = 0; nt < DVT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) t[(mw * DVT + nt) * 16 + r] = acc[mw][nt][r];
+    t[PER - 2] = zc[0];
+    t[PER - 1] = zc[1];
   }
 }
 
@@ -361,12 +393,29 @@ __global__ __launch_bounds__(256, DVT == 4 ? 1 : 2) void g32_out_kernel(const G3
 int dp32_of(int d) { return 16 * ((d + 15) / 16); }
 int dvt32_of(int dv) { return dv <= 32 ? 1 : dv <= 64 ? 2 : 4; }
 
+// Parts of the state sweep: when the (head, work-group) pairs fill less than half of 256 CUs,
+// enough parts for two work-groups per CU (the totals pass sweeps all but the last part a second
+// time, which pays only then), at least two segments per part.
+void g32_parts(int BH, int nwga, int nseg, int& nparts, int& spp) {
+  const int units = BH * nwga;
+  const int want = units < 128 ? (512 + units - 1) / units : 1;
+  nparts = max(1, min(want, (nseg - 1) / 2));
+  spp = (nseg - 1 + nparts - 1) / nparts;
+  nparts = (nseg - 1 + spp - 1) / spp;
+}
+
+// Workspace: T, z, then the part totals.
 template <int DP>
-size_t g32_bytes_dp(int BH, int nseg, int DVT) {
+size_t g32_bytes_dp(int BH, int nseg, int DVT, size_t* t_bytes = nullptr, size_t* z_bytes = nullptr) {
   constexpr int F = 16 * GFeat<DP>::NGP;
   const size_t nslot = (size_t)(nseg - 1) * BH;
   const auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  return up(nslot * F * (32 * DVT) * 4) + up(nslot * F * 4);
+  int nparts, spp;
+  g32_parts(BH, GFeat<DP>::NWGA, nseg, nparts, spp);
+  const size_t tb = up(nslot * F * (32 * DVT) * 4), zb = up(nslot * F * 4);
+  if (t_bytes) *t_bytes = tb;
+  if (z_bytes) *z_bytes = zb;
+  return tb + zb + up((size_t)(nparts - 1) * BH * GFeat<DP>::NWGA * 256 * (2 * DVT * 16 + 2) * 4);
 }
 
 size_t g32_bytes(int BH, int N, int d, int dv) {
@@ -383,7 +432,14 @@ size_t g32_bytes(int BH, int N, int d, int dv) {
 template <int DP, int DVT>
 int launch_g32(const G32Params& p, hipStream_t stream) {
   if (p.nseg > 1) {
-    hipLaunchKernelGGL((g32_state_kernel<DP, DVT>), dim3((unsigned)(p.BH * GFeat<DP>::NWGA)), dim3(256), 0, stream, p);
+    const unsigned units = (unsigned)(p.BH * GFeat<DP>::NWGA);
+    if (p.nparts > 1) {
+      hipLaunchKernelGGL((g32_state_kernel<DP, DVT, true>), dim3(units * (unsigned)(p.nparts - 1)), dim3(256), 0,
+                         stream, p);
+      const int e = (int)hipGetLastError();
+      if (e != 0) return e;
+    }
+    hipLaunchKernelGGL((g32_state_kernel<DP, DVT, false>), dim3(units * (unsigned)p.nparts), dim3(256), 0, stream, p);
     const int e = (int)hipGetLastError();
     if (e != 0) return e;
   }
@@ -429,11 +485,19 @@ int launch_general_chunked_f32(const ChunkedArgs& a, hipStream_t stream) {
     const size_t need = g32_bytes(a.BH, a.N, a.d, a.dv);
     if (a.workspace == nullptr || a.workspace_bytes < need) return LA_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(a.workspace) & 15) return LA_ERR_BAD_ALIGNMENT;
-    const int F = 16 * (DP == 16 ? GFeat<16>::NGP : DP == 32 ? GFeat<32>::NGP : DP == 48 ? GFeat<48>::NGP : GFeat<64>::NGP);
-    const size_t nslot = (size_t)(p.nseg - 1) * a.BH;
-    const size_t tb = (nslot * F * (32 * DVT) * 4 + 255) & ~(size_t)255;
-    p.T = static_cast<float*>(a.workspace);
-    p.Z = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + tb);
+    size_t tb = 0, zb = 0;
+    int nwga = 0;
+    switch (DP) {
+      case 16: g32_bytes_dp<16>(a.BH, p.nseg, DVT, &tb, &zb); nwga = GFeat<16>::NWGA; break;
+      case 32: g32_bytes_dp<32>(a.BH, p.nseg, DVT, &tb, &zb); nwga = GFeat<32>::NWGA; break;
+      case 48: g32_bytes_dp<48>(a.BH, p.nseg, DVT, &tb, &zb); nwga = GFeat<48>::NWGA; break;
+      default: g32_bytes_dp<64>(a.BH, p.nseg, DVT, &tb, &zb); nwga = GFeat<64>::NWGA; break;
+    }
+    g32_parts(a.BH, nwga, p.nseg, p.nparts, p.spp);
+    char* ws = static_cast<char*>(a.workspace);
+    p.T = reinterpret_cast<float*>(ws);
+    p.Z = reinterpret_cast<float*>(ws + tb);
+    p.Tot = reinterpret_cast<float*>(ws + tb + zb);
   }
   switch (DP) {
     case 16: return launch_g32_dp<16>(p, DVT, stream);

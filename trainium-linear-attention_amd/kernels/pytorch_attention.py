@@ -123,9 +123,9 @@ def ref_based_attn(q, k, v, eps=1e-6):
 CHUNKED_MIN_T = 256
 
 # Sequence length from which ``solution`` uses the segment-state chunked path for the other head
-# dims and for fp32 inputs (d <= 64, dv <= 128).  Measured on MI355X at N = 8192, B2 H16: bf16 d64
-# dv64 0.513 ms against 0.444 ms for the fused kernel, fp32 d16 dv64 1.21 against 1.45 ms, fp32
-# d64 2.48 against 2.29 ms; the fused kernel's work grows with N^2, the chunked paths' with N.
+# dims and for fp32 inputs (d <= 64, dv <= 128).  Measured on MI355X at N = 8192, B2 H16 (whole
+# calls, ms, chunked / fused): bf16 d64 dv64 0.435 / 0.451, bf16 d32 dv128 0.517 / 0.511, fp32
+# d16 dv64 0.774 / 1.455; the fused kernel's work grows with N^2, the chunked paths' with N.
 GENERAL_CHUNKED_MIN_T = 16384
 
 
