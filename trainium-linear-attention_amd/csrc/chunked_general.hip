@@ -91,8 +91,8 @@ __device__ __forceinline__ int gswz(int row, int unit) { return (unit ^ ((row >>
 // One work-group per (head, 64-token chunk) of the tokens before the last segment.  Per token t:
 // n_t = 2^e >= max(max_i |k_ti|, 1), k~ = [k, 1] / n_t in fp16 (every entry in [-1, 1]); the
 // token's features are then phi(k~) = phi([k, 1]) / n_t^2, so the V^T rows carry v n_t^2 and the
-// z row n_t^2, each scaled by a power of two of the chunk (Ec, Ez: the chunk's largest value in
-// [2^14, 2^15)), written to CE[head][chunk] = {Ec, Ez}.
+// z row n_t^2, each scaled by a power of two of the chunk (Ec, Ez, multiples of 8: the chunk's
+// largest value in [2^7, 2^15)), written to CE[head][chunk] = {Ec, Ez}.
 template <int DP, int DVT>
 __global__ __launch_bounds__(256) void gprep_kernel(const GParams p) {
   using CK = GChunk<DP, DVT>;
@@ -163,8 +163,11 @@ __global__ __launch_bounds__(256) void gprep_kernel(const GParams p) {
   __syncthreads();
   cv = max(max(red[0][0], red[0][1]), max(red[0][2], red[0][3]));
   cz = max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3]));
-  const int Ec = cv == 0u ? 0 : (int)(cv >> 23) - 127 - 14;
-  const int Ez = 2 * (int)cz - 14;
+  // exponents in steps of 8 (largest value in [2^7, 2^15)), so that chunks of one order of
+  // magnitude share them and the state kernel scales nothing
+  const int ev = cv == 0u ? -1000 : (int)(cv >> 23) - 127;   // chunk max of |v| n^2 in [2^ev, 2^(ev+1))
+  const int Ec = cv == 0u ? 0 : 8 * ((ev - 14 + 7 + 1024) / 8 - 128);
+  const int Ez = 8 * ((2 * (int)cz - 1 - 14 + 7 + 1024) / 8 - 128);
   const float sv = __builtin_ldexpf(1.0f, 2 * en - Ec), sz = __builtin_ldexpf(1.0f, 2 * en - Ez);
 
   // rows into LDS, [row][64 tokens] unswizzled
