@@ -240,10 +240,25 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ u32 swap16(u32 x) { return __builtin_amdgcn_alignbit(x, x, 16); }
 
-// Half index of the 16-byte unit u (tokens 8u .. 8u + 7) of V^T row c.  The XOR spreads the
-// staging stores (8 rows 8 apart per instruction) over all banks; MFMA operand reads (16
-// consecutive rows, one unit) stay conflict-free.
-__device__ __forceinline__ int vt_off(int c, int u) { return c * KRS + 8 * (u ^ (2 * (c >> 4))); }
+// Half index of the 16-byte unit u (tokens 8u .. 8u + 7) of V^T row c.  Rows are 17 units apart
+// and row c = 8 j + e (j = c / 8) is stored at row position 8 j + (e ^ (j mod 8)), so unit u of
+// row c sits in 16-byte bank group (8 j + (e ^ j) + u) mod 16.  On gfx950 (64 dword banks; as
+// measured with SQ_LDS_BANK_CONFLICT):
+//   * ds_read_b128 serves a wave in four passes of 16 lanes, lanes l with the same l >> 5 and
+//     the same parity of bits 2..4 of l; the MFMA operand reads (lane r reads row 32 n + r at
+//     one unit) then take 16 rows in distinct bank groups in every pass;
+//   * ds_write_b32 serves 32 lanes per pass over 32 dword banks; the staging stores (rows 8 j + e
+//     for j = 0..7 at one e, four token pairs each) land at dword 4 (((e ^ j) + u) mod 8) + t,
+//     distinct over j and t.
+// A row keeps its units in order, so every read is a per-lane base plus an immediate offset.
+__device__ __forceinline__ int vt_row(int c) { return (c & ~7) | ((c ^ (c >> 3)) & 7); }
+__device__ __forceinline__ int vt_off(int c, int u) { return vt_row(c) * KRS + 8 * u; }
+
+// Row position of K^T row `row`: rows 8..15 rotated by two within their octet.  The staging
+// stores (ds_write_b32, 32 lanes per pass over 32 dword banks) write rows d0 + i for d0 = 0, 4,
+// 8, 12 at once, eight token pairs each; rows 8 apart (17 units) would share banks, rotated they
+// fill all 32.  The feature reads keep their bank spread (rows 8..15 stay in bank groups 8..15).
+__device__ __forceinline__ int kt_row(int row) { return (row & ~7) == 8 ? 8 + ((row + 2) & 7) : row; }
 
 // Constant rows of the K^T table (written once per kernel).
 __device__ __forceinline__ void init_kt_constants(uint16_t* KT, int tid, int nthreads) {
@@ -507,7 +522,7 @@ __device__ __forceinline__ void stage_write(const StageConv& o, uint16_t* Q0, ui
     const int tp = 16 * wv + (l >> 2);                       // token pair
     const int d0 = 8 * (l & 1) + 4 * ((l >> 1) & 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32*>(&KT[(d0 + i) * KRS + 2 * tp]) = o.kt[i];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32*>(&KT[kt_row(d0 + i) * KRS + 2 * tp]) = o.kt[i];
   }
   stage_write_v(o, VT, l, wv);
 }
@@ -586,8 +601,8 @@ __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_k
   const bool stager = w < 4 && active;
 
   const KRows kr = krows(block_slot(w, r));
-  const int ra[1] = {kr.a * KRS}, rb[1] = {kr.b * KRS};
-  const int grow = gram_row(r) * KRS;
+  const int ra[1] = {kt_row(kr.a) * KRS}, rb[1] = {kt_row(kr.b) * KRS};
+  const int grow = kt_row(gram_row(r)) * KRS;
   f32x16 S[1][2] = {{splat16(0.f), splat16(0.f)}};
   f32x16 G = splat16(0.f);
 
@@ -1096,10 +1111,10 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     const KRows kr = krows(block_slot(OB::first + b, r));
-    ra[b] = kr.a * KRS;
-    rb[b] = kr.b * KRS;
+    ra[b] = kt_row(kr.a) * KRS;
+    rb[b] = kt_row(kr.b) * KRS;
   }
-  const int grow = gram_row(r) * KRS;
+  const int grow = kt_row(gram_row(r)) * KRS;
   // causal mask of the diagonal score tile: element e of lane (query r, half h) is key
   // 16 (e >> 3) + 8 h + (e & 7); packed pairs keep a half iff key <= r
   u32 dmask[8];

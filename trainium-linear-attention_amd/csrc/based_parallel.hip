@@ -87,6 +87,12 @@ constexpr int VR = 64;    // partial maxima of |v| per head (vrange_kernel)
 
 constexpr int NRAW = 7;   // LDS stages of the packed path
 
+// Swizzle bit of a key's two 16-byte K chunks in a packed stage: the score operand read (lane
+// n, h takes chunk h of key 32 ks + n) then touches 16 distinct 16-byte units mod 16 in every
+// group of 16 lanes, i.e. all 64 banks once per 16-lane pass of ds_read_b128 (bit 2 alone left
+// keys n and n + 8 on the same banks).
+__device__ __forceinline__ int kswz(int key) { return ((key >> 2) ^ (key >> 3)) & 1; }
+
 template <int DV>
 using VtBlockP = VtBlock<DV, VROW>;
 
@@ -194,8 +200,8 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   for (int i = 0; i < UPW; ++i) {
     const int u = wu + NW * i;
     if (u < 2) {
-      // K slot sl = 2 key + (c ^ ((key >> 2) & 1)) holds 16-byte chunk c of the key's row
-      const int sl = 64 * u + lane, key = sl >> 1, c = (sl & 1) ^ ((key >> 2) & 1);
+      // K slot sl = 2 key + (c ^ kswz(key)) holds 16-byte chunk c of the key's row
+      const int sl = 64 * u + lane, key = sl >> 1, c = (sl & 1) ^ kswz(key);
       uoff[i] = key * 32 + 16 * c;
     } else {
       uoff[i] = 1024 * (u - 2) + 16 * lane;
@@ -249,7 +255,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   auto kfrag = [&](int j, int ks, int kk) -> u32x4 {
     const int key = 32 * ks + n;
     if (PACKED) {
-      const int sl = 2 * key + (h ^ ((key >> 2) & 1));
+      const int sl = 2 * key + (h ^ kswz(key));
       return *reinterpret_cast<const u32x4*>(&stage[j % NRAW][8 * sl]);
     }
     return *reinterpret_cast<const u32x4*>(&Ks[j & 1][key * KROW + 16 * kk + 8 * h]);
