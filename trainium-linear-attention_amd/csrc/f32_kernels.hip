@@ -39,6 +39,7 @@ struct F32Params {
                          // [BH][nslot][BM] (null: no split)
   int BH, N, d, dv, nqb, window, nslot;
   int vec;               // d % 4 == 0, dv % 4 == 0 and q, k, v 16-byte aligned: float4 loads
+  int out_vec;           // out 16-byte (fp32) / 8-byte (bf16) aligned: 4-column stores
   float inv_c, inv_c2, fscale, eps, scale_log2;
   int normalize, out_f32;
 };
@@ -370,10 +371,247 @@ __global__ __launch_bounds__(256) void f32_split_combine_kernel(const F32Params 
   }
 }
 
+// fp32 BASED for small grids on bf16 MFMAs (d <= 16, dv <= 64, q / k / v rows 16-byte aligned).
+// Every fp32 operand x is carried as three bf16 terms, x = x0 + x1 + x2 with x0 = bf16(x),
+// x1 = bf16(x - x0), x2 = bf16(x - x0 - x1) (the differences are exact in fp32; the three terms
+// hold x's 24-bit significand), and every product as the six bf16 MFMAs of term pairs (i, j)
+// with i + j <= 2 (the dropped ones are below 2^-24 of the product), accumulated in fp32: the
+// scores S^T = K Q^T (started from 1/c, as in f32_attn_kernel) and O^T = V^T P^T.  One 32x32x16
+// bf16 MFMA does the work of eight 32x32x2 fp32 ones in half their cycles, so the six of a
+// product cost 3/8 of the fp32 form, and no second pass adds partial sums.
+//
+// Work-group (head, 32 queries q0 .. q0 + 31), 8 waves: wave w takes the 32-key tiles u = w,
+// w + 8, ... up to the queries' own (diagonal) tile.  Per tile it loads the K and V rows (fp32,
+// 1 KB per load instruction) into registers one tile ahead, splits them and stores the three
+// terms row-major in its own LDS region (16-byte chunks XOR-swizzled by row), reads the K
+// fragments with ds_read_b128 and the V^T fragments with ds_read_b64_tr_b16 (as in the resident
+// sliding-window kernel: the key order of a V^T fragment is the accumulator row order of the
+// score tile, so P^T needs no shuffle).  At the end the waves' numerators and row sums are added
+// through LDS in wave order (deterministic) and wave 0 normalises and stores.
+struct Split3 {
+  u32 t[3];
+};
+__device__ __forceinline__ Split3 split3_bf16x2(float a, float b) {
+  Split3 r;
+  r.t[0] = pack_bf16x2(a, b);
+  const float ra = a - bf16_lo_to_f32(r.t[0]), rb = b - bf16_hi_to_f32(r.t[0]);
+  r.t[1] = pack_bf16x2(ra, rb);
+  r.t[2] = pack_bf16x2(ra - bf16_lo_to_f32(r.t[1]), rb - bf16_hi_to_f32(r.t[1]));
+  return r;
+}
+
+// acc += A B over the term pairs (i, j), i + j <= 2, smallest first
+__device__ __forceinline__ f32x16 mfma_split3(const u32x4 (&a)[3], const u32x4 (&b)[3], f32x16 acc) {
+  acc = mfma32x32x16(a[1], b[1], acc);
+  acc = mfma32x32x16(a[2], b[0], acc);
+  acc = mfma32x32x16(a[0], b[2], acc);
+  acc = mfma32x32x16(a[1], b[0], acc);
+  acc = mfma32x32x16(a[0], b[1], acc);
+  return mfma32x32x16(a[0], b[0], acc);
+}
+
+template <int MT>
+__global__ __launch_bounds__(512) void f32_x6_kernel(const F32Params p) {
+  constexpr int NW = 8, DV = 32 * MT, KT = 32;
+  constexpr int VCH = DV / 8;                 // 16-byte chunks per V row (bf16)
+  constexpr int VP = KT * DV / 4 / 64;        // f32x4 pieces of a V tile per lane
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  // per wave and term: K rows [KT][16], then V rows [KT][DV] (bf16)
+  constexpr int TAB = KT * 16 + KT * DV;
+  __shared__ __attribute__((aligned(16))) uint16_t tabs[NW * 3 * TAB];
+  static_assert(NW * 64 * (MT * 16 + 1) * 4 <= (int)sizeof(tabs), "reduction fits");
+
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, n = lane & 31, gh = (lane >> 4) & 1, gi = lane & 15;
+  const int N = p.N, d = p.d, dv = p.dv;
+  int bh, qb;
+  map_causal_block(blockIdx.x, p.BH, p.nqb, bh, qb);
+  const int q0 = KT * qb, query = q0 + n;
+  const int ud = min(qb, (N - 1) / KT);   // the diagonal tile
+  const size_t hrow = (size_t)bh * N;
+  const float* __restrict__ qg = p.q + hrow * d;
+  const float* __restrict__ kg = p.k + hrow * d;
+  const float* __restrict__ vg = p.v + hrow * dv;
+  uint16_t* const mine = tabs + 3 * w * TAB;
+
+  // Q^T fragment: lane (query n, half h) holds dims 8h .. 8h + 7, as three terms
+  u32x4 qf[3];
+  {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 4) {
+      const int col = 8 * h + e;
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+      if (query < N && col < d) t = *reinterpret_cast<const f32x4*>(qg + (size_t)query * d + col);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[e + i] = t[i];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const Split3 t = split3_bf16x2(x[2 * c], x[2 * c + 1]);
+#pragma unroll
+      for (int r = 0; r < 3; ++r) qf[r][c] = t.t[r];
+    }
+  }
+
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = splat16(0.f);
+  float rsum = 0.f;
+
+  // raw tile in registers: K piece i = key 16 i + lane / 4, dims 4 (lane % 4) .. +3; V piece i =
+  // key (64 i + lane) / (DV / 4), columns 4 ((64 i + lane) % (DV / 4)) .. +3
+  f32x4 kr[2], vr[VP];
+  auto load = [&](int u) {
+    const int kb = KT * u;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = kb + 16 * i + (lane >> 2), col = 4 * (lane & 3);
+      f32x4 x = {0.f, 0.f, 0.f, 0.f};
+      if (key < N && col < d) x = *reinterpret_cast<const f32x4*>(kg + (size_t)key * d + col);
+      kr[i] = x;
+    }
+#pragma unroll
+    for (int i = 0; i < VP; ++i) {
+      const int c = 64 * i + lane, key = kb + c / (DV / 4), col = 4 * (c % (DV / 4));
+      f32x4 x = {0.f, 0.f, 0.f, 0.f};
+      if (key < N && col < dv) x = *reinterpret_cast<const f32x4*>(vg + (size_t)key * dv + col);
+      vr[i] = x;
+    }
+  };
+  auto put = [&](int off, const f32x4& x) {
+    const Split3 a = split3_bf16x2(x[0], x[1]), b = split3_bf16x2(x[2], x[3]);
+#pragma unroll
+    for (int r = 0; r < 3; ++r) *reinterpret_cast<u32x2*>(&mine[r * TAB + off]) = (u32x2){a.t[r], b.t[r]};
+  };
+  // K row r: 16-byte chunk c at position c ^ bit 4 of r (the fragment reads of rows n, chunk h
+  // then fill all bank groups per pass); V row r: chunk c at c ^ ((r >> 1) mod VCH)
+  auto store = [&]() {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = 16 * i + (lane >> 2), col4 = lane & 3;
+      put(key * 16 + 8 * ((col4 >> 1) ^ ((key >> 4) & 1)) + 4 * (col4 & 1), kr[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < VP; ++i) {
+      const int c = 64 * i + lane, key = c / (DV / 4), col4 = c % (DV / 4);
+      put(KT * 16 + key * DV + 8 * ((col4 >> 1) ^ ((key >> 1) % VCH)) + 4 * (col4 & 1), vr[i]);
+    }
+  };
+  const float inv_c = p.inv_c, inv_c2 = p.inv_c2, fscale = p.fscale;
+  auto tile = [&](int u) {
+    const int kb = KT * u;
+    u32x4 kf[3];
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+      kf[r] = *reinterpret_cast<const u32x4*>(&mine[r * TAB + n * 16 + 8 * (h ^ ((n >> 4) & 1))]);
+    const f32x16 b = mfma_split3(kf, qf, splat16(inv_c));
+    // element i of lane (query n, half h) is key kb + c32_row(i, h)
+    const bool interior = kb + KT - 1 <= q0 && kb + KT <= N;   // every key before every query
+    float pr[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = kb + c32_row(i, h);
+      const float uu = __builtin_fmaf(b[i], b[i], -inv_c2);
+      const float pe = __builtin_fmaf(fscale, uu, 1.0f);
+      pr[i] = (interior || (key <= query && key < N)) ? pe : 0.f;
+      rsum += pr[i];
+    }
+    u32x4 pf[2][3];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const Split3 s3 = split3_bf16x2(pr[8 * m + 2 * c], pr[8 * m + 2 * c + 1]);
+#pragma unroll
+        for (int r = 0; r < 3; ++r) pf[m][r][c] = s3.t[r];
+      }
+    // V^T fragment (m): keys 16 m + 8 (e / 4) + 4 h + e % 4 of element e, two transposed reads of
+    // rows 16 m + 8 s2 + 4 h + 0..3 per term
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        u32x4 vf[3];
+#pragma unroll
+        for (int r = 0; r < 3; ++r) {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            const int row = 16 * m + 8 * s2 + 4 * h + (gi >> 2);
+            const int col = 32 * mt + 16 * gh + 4 * (gi & 3);
+            const uint16_t* src = &mine[r * TAB + KT * 16 + row * DV + 8 * ((col >> 3) ^ ((row >> 1) % VCH)) + (col & 7)];
+            const v4s r4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)src);
+            const u32x2 r2 = __builtin_bit_cast(u32x2, r4);
+            vf[r][2 * s2] = r2[0];
+            vf[r][2 * s2 + 1] = r2[1];
+          }
+        }
+        acc[mt] = mfma_split3(vf, pf[m], acc[mt]);
+      }
+  };
+
+  if (w <= ud) load(w);
+  for (int u = w; u <= ud; u += NW) {
+    store();   // this wave's region; its reads of the previous tile were issued before (in order)
+    if (u + NW <= ud) load(u + NW);
+    tile(u);
+  }
+
+  // wave-ordered sum of the numerators and row sums (the tables are free after the barrier)
+  const int nact = min(NW, ud + 1);
+  float* red = reinterpret_cast<float*>(tabs);
+  __syncthreads();
+  if (w > 0 && w < nact) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) red[((w * MT + mt) * 16 + i) * 64 + lane] = acc[mt][i];
+    red[(NW * MT * 16 + w) * 64 + lane] = rsum;
+  }
+  __syncthreads();
+  if (w != 0) return;
+  for (int ww = 1; ww < nact; ++ww) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mt][i] += red[((ww * MT + mt) * 16 + i) * 64 + lane];
+    rsum += red[(NW * MT * 16 + ww) * 64 + lane];
+  }
+  const float rs = rsum + __shfl_xor(rsum, 32);
+  if (query >= N) return;
+  const float inv = p.normalize ? 1.0f / (rs + p.eps) : 1.0f;
+  if (p.den != nullptr && h == 0) p.den[hrow + query] = rs;
+  const size_t obase = (hrow + query) * (size_t)dv;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int col = 32 * mt + 8 * g + 4 * h;
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = acc[mt][4 * g + e] * inv;
+      if (col < dv) {
+        if (p.out_f32)
+          *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + obase + col) = (f32x4){y[0], y[1], y[2], y[3]};
+        else
+          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + obase + col) =
+              (u32x2){pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+      }
+    }
+}
+
 template <int KS, int MT, bool SL>
 int launch_f32(F32Params p, hipStream_t stream) {
   p.nqb = (p.N + 127) / 128;
   const dim3 grid((unsigned)(p.nqb * p.BH));
+  if constexpr (!SL && KS == 1 && MT <= 2) {
+    // small grids (the key-split condition) with 16-byte rows: three-term bf16 products, one launch
+    if (p.part != nullptr && p.vec && p.out_vec) {
+      p.nqb = (p.N + 31) / 32;
+      hipLaunchKernelGGL(f32_x6_kernel<MT>, dim3((unsigned)(p.nqb * p.BH)), dim3(512), 0, stream, p);
+      return (int)hipGetLastError();
+    }
+  }
   if constexpr (!SL) {
     if (p.part != nullptr) {
       // key split over work-groups (the workspace was sized for it: f32_split_slots)
@@ -449,6 +687,7 @@ int launch_based_parallel_fp32(const ParallelArgs& a, hipStream_t stream) {
   p.out_f32 = a.out_f32 ? 1 : 0;
   p.vec = (a.d % 4 == 0) && (a.dv % 4 == 0) && ((reinterpret_cast<uintptr_t>(a.q) & 15) == 0) &&
           ((reinterpret_cast<uintptr_t>(a.k) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 15) == 0);
+  p.out_vec = (reinterpret_cast<uintptr_t>(a.out) & (a.out_f32 ? 15 : 7)) == 0;
   p.nslot = f32_split_slots(a.BH, a.N);
   if (p.nslot > 0) {
     if (a.workspace == nullptr || a.workspace_bytes < f32_split_workspace_bytes(a.BH, a.N, a.dv))
