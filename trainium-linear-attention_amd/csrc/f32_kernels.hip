@@ -433,6 +433,9 @@ __global__ __launch_bounds__(512) void f32_x6_kernel(const F32Params p) {
   const float* __restrict__ kg = p.k + hrow * d;
   const float* __restrict__ vg = p.v + hrow * dv;
   uint16_t* const mine = tabs + 3 * w * TAB;
+  // V row r keeps 16-byte chunk c at c ^ (4 bit1(r)) when it has 8 chunks: the transposed reads
+  // of rows r .. r + 3 (four chunks each, 32 lanes per pass) then cover all 64 banks
+  auto vswz = [](int r) { return VCH >= 8 ? ((r >> 1) & 1) << 2 : 0; };
 
   // Q^T fragment: lane (query n, half h) holds dims 8h .. 8h + 7, as three terms
   u32x4 qf[3];
@@ -485,7 +488,7 @@ __global__ __launch_bounds__(512) void f32_x6_kernel(const F32Params p) {
     for (int r = 0; r < 3; ++r) *reinterpret_cast<u32x2*>(&mine[r * TAB + off]) = (u32x2){a.t[r], b.t[r]};
   };
   // K row r: 16-byte chunk c at position c ^ bit 4 of r (the fragment reads of rows n, chunk h
-  // then fill all bank groups per pass); V row r: chunk c at c ^ ((r >> 1) mod VCH)
+  // then fill all bank groups per pass); V rows: vswz
   auto store = [&]() {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -495,7 +498,7 @@ __global__ __launch_bounds__(512) void f32_x6_kernel(const F32Params p) {
 #pragma unroll
     for (int i = 0; i < VP; ++i) {
       const int c = 64 * i + lane, key = c / (DV / 4), col4 = c % (DV / 4);
-      put(KT * 16 + key * DV + 8 * ((col4 >> 1) ^ ((key >> 1) % VCH)) + 4 * (col4 & 1), vr[i]);
+      put(KT * 16 + key * DV + 8 * ((col4 >> 1) ^ vswz(key)) + 4 * (col4 & 1), vr[i]);
     }
   };
   const float inv_c = p.inv_c, inv_c2 = p.inv_c2, fscale = p.fscale;
@@ -539,7 +542,7 @@ __global__ __launch_bounds__(512) void f32_x6_kernel(const F32Params p) {
           for (int s2 = 0; s2 < 2; ++s2) {
             const int row = 16 * m + 8 * s2 + 4 * h + (gi >> 2);
             const int col = 32 * mt + 16 * gh + 4 * (gi & 3);
-            const uint16_t* src = &mine[r * TAB + KT * 16 + row * DV + 8 * ((col >> 3) ^ ((row >> 1) % VCH)) + (col & 7)];
+            const uint16_t* src = &mine[r * TAB + KT * 16 + row * DV + 8 * ((col >> 3) ^ vswz(row)) + (col & 7)];
             const v4s r4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)src);
             const u32x2 r2 = __builtin_bit_cast(u32x2, r4);
             vf[r][2 * s2] = r2[0];

@@ -41,8 +41,10 @@ struct IdentityParams {
 constexpr int kIdNW = 8;      // waves per work-group
 constexpr int kIdBlocks = 4;  // 64-token blocks per work-group
 
-__device__ __forceinline__ int id_swz_k(int row, int nch) { return row % nch; }
-__device__ __forceinline__ int id_swz_v(int row, int nch) { return (row >> 1) % nch; }
+// Chunk swizzles for gfx950's LDS banks (as in the resident sliding-window kernel): K rows keep
+// chunk c at c ^ ((row nch / 16) mod nch), V rows of 8 chunks at c ^ (4 bit1(row)).
+__device__ __forceinline__ int id_swz_k(int row, int nch) { return ((row * nch) >> 4) % nch; }
+__device__ __forceinline__ int id_swz_v(int row, int nch) { return nch >= 8 ? ((row >> 1) & 1) << 2 : 0; }
 
 template <int KS, int MT, bool STATE>
 __global__ __launch_bounds__(64 * kIdNW) __attribute__((amdgpu_waves_per_eu(KS * MT <= 2 ? 6 : 2))) void identity_kernel(

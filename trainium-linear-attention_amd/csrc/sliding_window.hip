@@ -211,8 +211,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS == 8 ? 1
 // k0 .. k0 + 3.  Everything else (masking, online softmax, hi/lo split of P) is as in
 // sliding_bf16_kernel.
 
-__device__ __forceinline__ int swz_k(int row, int nch) { return row % nch; }
-__device__ __forceinline__ int swz_v(int row, int nch) { return (row >> 1) % nch; }
+// Chunk swizzles for gfx950's LDS (64 dword banks; ds_read_b128 serves lanes with equal lane >> 5
+// and equal parity of lane bits 2..4 in one pass, ds_read_b64_tr_b16 32 consecutive lanes): K row
+// `row` of nch 16-byte chunks keeps chunk c at c ^ ((row nch / 16) mod nch), so the fragment reads
+// (lane n reads row n) put the 16 rows of a pass in distinct bank groups; a V row of 8 chunks
+// keeps chunk c at c ^ (4 bit1(row)), so the transposed reads of rows r .. r + 3 (four chunks
+// each) cover all 64 banks (rows of 4 chunks need no swizzle).
+__device__ __forceinline__ int swz_k(int row, int nch) { return ((row * nch) >> 4) % nch; }
+__device__ __forceinline__ int swz_v(int row, int nch) { return nch >= 8 ? ((row >> 1) & 1) << 2 : 0; }
 
 template <int KS, int MT, int NW, int XB>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 8 ? 4 : 3))) void sliding_resident_kernel(
