@@ -267,3 +267,37 @@ def test_fp32_key_split(B, H, N, d, dv):
 def _lib_mod():
     from kernels import _lib
     return _lib
+
+
+@pytest.mark.parametrize("N,d,dv", [(129, 16, 64), (200, 4, 8), (777, 12, 36), (1024, 8, 64), (1000, 16, 32),
+                                    (300, 16, 4), (2047, 16, 64)])
+def test_fp32_small_grid_three_term_kernel(N, d, dv):
+    """fp32 on small grids (d <= 16, dv <= 64, aligned rows): three-term bf16 products.  Normalised
+    output, numerator and row sums against fp64 at the fp32 bar; a bf16 output equal to the
+    rounded fp32 one; and a misaligned output (the key-split kernel with its combine) equal to the
+    fp32 bar too."""
+    K = _kernels()
+    q, k, v = rand_qkv(1, 3, N, d, dv, seed=N + d + dv, dtype=torch.float32, scale_qk=1.0)
+    qd, kd, vd = to_dev(q, k, v)
+    want, want_num, want_den = ref.based_dense(q, k, v)
+    y, den = K.based_parallel(qd, kd, vd, out_dtype=torch.float32, return_den=True)
+    num = K.based_parallel(qd, kd, vd, normalize=False, out_dtype=torch.float32)
+    e, en, ed = err(y, want), err(num, want_num), err(den, want_den)
+    print(f"fp32 small grid N={N} d={d} dv={dv} err={e:.3e} num={en:.3e} den={ed:.3e}")
+    assert e < TOL_F32 and en < TOL_F32 and ed < TOL_F32
+    yb = K.based_parallel(qd, kd, vd, out_dtype=torch.bfloat16)
+    assert torch.equal(yb, y.to(torch.bfloat16))
+    # an output 4 bytes off 16-byte alignment takes the key-split kernel
+    buf = torch.empty(y.numel() + 1, dtype=torch.float32, device="cuda")
+    y2 = buf[1:].view_as(y)
+    from kernels import _lib
+    L = _lib.lib()
+    B, H = 1, 3
+    ws_bytes = int(L.la_based_parallel_workspace_bytes(B, H, N, d, dv, 0))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    rc = L.la_based_parallel_fwd(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), 0, y2.data_ptr(), 0, 0, B, H, N, d, dv,
+                                 1.0 / math.sqrt(d), 1e-6, 1, ws.data_ptr(), ws_bytes,
+                                 torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert err(y2, want) < TOL_F32
