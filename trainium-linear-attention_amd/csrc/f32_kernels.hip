@@ -603,6 +603,178 @@ __global__ __launch_bounds__(512) void f32_x6_kernel(const F32Params p) {
     }
 }
 
+// fp32 BASED on larger grids, with the three-term bf16 products of f32_x6_kernel: work-group
+// (head, 128 queries), wave w owns queries q0 + 32 w .. +31 and all DV columns.  The 32-key
+// tiles of K and V pass through LDS once per work-group as their three bf16 terms (K rows
+// [3][32][16], V rows [3][32][DV], double-buffered): each thread loads one K piece and DV / 32
+// V pieces of the next tile into registers while the current one is computed, then splits and
+// stores them behind one barrier per tile.  Scores, the causal mask, p, its split and
+// O^T += V^T P^T are as in f32_x6_kernel; every wave finishes its own queries (no reduction).
+template <int MT, int NW>
+__global__ __launch_bounds__(64 * NW) void f32_x6_tiled_kernel(const F32Params p) {
+  constexpr int DV = 32 * MT, KT = 32, BM = 32 * NW, NT = 64 * NW;
+  constexpr int VCH = DV / 8;
+  constexpr int VP = (KT * DV / 4 + NT - 1) / NT;   // V float4 pieces of a tile per thread
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  constexpr int TAB = KT * 16 + KT * DV;      // halves per term: K rows, then V rows
+  __shared__ __attribute__((aligned(16))) uint16_t tabs[2][3 * TAB];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, n = lane & 31, gh = (lane >> 4) & 1, gi = lane & 15;
+  const int N = p.N, d = p.d, dv = p.dv;
+  int bh, qb;
+  map_causal_block(blockIdx.x, p.BH, p.nqb, bh, qb);
+  const int q0 = BM * qb, wq0 = q0 + 32 * w, query = wq0 + n;
+  const bool wave_live = wq0 < N;
+  const int ud = min((q0 + BM - 1) / KT, (N - 1) / KT);   // last tile with a key <= a query
+  const size_t hrow = (size_t)bh * N;
+  const float* __restrict__ qg = p.q + hrow * d;
+  const float* __restrict__ kg = p.k + hrow * d;
+  const float* __restrict__ vg = p.v + hrow * dv;
+  auto vswz = [](int r) { return VCH >= 8 ? ((r >> 1) & 1) << 2 : 0; };
+
+  u32x4 qf[3];
+  {
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 4) {
+      const int col = 8 * h + e;
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+      if (query < N && col < d) t = *reinterpret_cast<const f32x4*>(qg + (size_t)query * d + col);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[e + i] = t[i];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const Split3 t = split3_bf16x2(x[2 * c], x[2 * c + 1]);
+#pragma unroll
+      for (int r = 0; r < 3; ++r) qf[r][c] = t.t[r];
+    }
+  }
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = splat16(0.f);
+  float rsum = 0.f;
+
+  // next tile in registers: K piece = key tid / 4, dims 4 (tid % 4) (threads < 128); V piece i =
+  // key (tid + NT i) / (DV / 4), columns 4 ((tid + NT i) % (DV / 4))
+  f32x4 kr, vr[VP];
+  auto load = [&](int u) {
+    const int kb = KT * u;
+    {
+      const int key = kb + (tid >> 2), col = 4 * (tid & 3);
+      f32x4 x = {0.f, 0.f, 0.f, 0.f};
+      if (tid < 128 && key < N && col < d) x = *reinterpret_cast<const f32x4*>(kg + (size_t)key * d + col);
+      kr = x;
+    }
+#pragma unroll
+    for (int i = 0; i < VP; ++i) {
+      const int c = tid + NT * i, key = kb + c / (DV / 4), col = 4 * (c % (DV / 4));
+      f32x4 x = {0.f, 0.f, 0.f, 0.f};
+      if (c < KT * DV / 4 && key < N && col < dv) x = *reinterpret_cast<const f32x4*>(vg + (size_t)key * dv + col);
+      vr[i] = x;
+    }
+  };
+  auto put = [&](uint16_t* t3, int off, const f32x4& x) {
+    const Split3 a = split3_bf16x2(x[0], x[1]), b = split3_bf16x2(x[2], x[3]);
+#pragma unroll
+    for (int r = 0; r < 3; ++r) *reinterpret_cast<u32x2*>(&t3[r * TAB + off]) = (u32x2){a.t[r], b.t[r]};
+  };
+  auto store = [&](int buf) {
+    uint16_t* t3 = tabs[buf];
+    if (tid < 128) {
+      const int key = tid >> 2, col4 = tid & 3;
+      put(t3, key * 16 + 8 * ((col4 >> 1) ^ ((key >> 4) & 1)) + 4 * (col4 & 1), kr);
+    }
+#pragma unroll
+    for (int i = 0; i < VP; ++i) {
+      const int c = tid + NT * i, key = c / (DV / 4), col4 = c % (DV / 4);
+      if (c < KT * DV / 4) put(t3, KT * 16 + key * DV + 8 * ((col4 >> 1) ^ vswz(key)) + 4 * (col4 & 1), vr[i]);
+    }
+  };
+  const float inv_c = p.inv_c, inv_c2 = p.inv_c2, fscale = p.fscale;
+  auto tile = [&](int buf, int u) {
+    const uint16_t* t3 = tabs[buf];
+    const int kb = KT * u;
+    u32x4 kf[3];
+#pragma unroll
+    for (int r = 0; r < 3; ++r)
+      kf[r] = *reinterpret_cast<const u32x4*>(&t3[r * TAB + n * 16 + 8 * (h ^ ((n >> 4) & 1))]);
+    const f32x16 b = mfma_split3(kf, qf, splat16(inv_c));
+    const bool interior = kb + KT - 1 <= wq0 && kb + KT <= N;
+    float pr[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = kb + c32_row(i, h);
+      const float uu = __builtin_fmaf(b[i], b[i], -inv_c2);
+      const float pe = __builtin_fmaf(fscale, uu, 1.0f);
+      pr[i] = (interior || (key <= query && key < N)) ? pe : 0.f;
+      rsum += pr[i];
+    }
+    u32x4 pf[2][3];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const Split3 s3 = split3_bf16x2(pr[8 * m + 2 * c], pr[8 * m + 2 * c + 1]);
+#pragma unroll
+        for (int r = 0; r < 3; ++r) pf[m][r][c] = s3.t[r];
+      }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        u32x4 vf[3];
+#pragma unroll
+        for (int r = 0; r < 3; ++r) {
+#pragma unroll
+          for (int s2 = 0; s2 < 2; ++s2) {
+            const int row = 16 * m + 8 * s2 + 4 * h + (gi >> 2);
+            const int col = 32 * mt + 16 * gh + 4 * (gi & 3);
+            const uint16_t* src = &t3[r * TAB + KT * 16 + row * DV + 8 * ((col >> 3) ^ vswz(row)) + (col & 7)];
+            const v4s r4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)src);
+            const u32x2 r2 = __builtin_bit_cast(u32x2, r4);
+            vf[r][2 * s2] = r2[0];
+            vf[r][2 * s2 + 1] = r2[1];
+          }
+        }
+        acc[mt] = mfma_split3(vf, pf[m], acc[mt]);
+      }
+  };
+
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int u = 0; u <= ud; ++u) {
+    if (u < ud) load(u + 1);
+    if (wave_live && KT * u <= wq0 + 31) tile(u & 1, u);
+    if (u < ud) store((u + 1) & 1);
+    __syncthreads();
+  }
+
+  if (!wave_live || query >= N) return;
+  const float rs = rsum + __shfl_xor(rsum, 32);
+  const float inv = p.normalize ? 1.0f / (rs + p.eps) : 1.0f;
+  if (p.den != nullptr && h == 0) p.den[hrow + query] = rs;
+  const size_t obase = (hrow + query) * (size_t)dv;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int col = 32 * mt + 8 * g + 4 * h;
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = acc[mt][4 * g + e] * inv;
+      if (col < dv) {
+        if (p.out_f32)
+          *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + obase + col) = (f32x4){y[0], y[1], y[2], y[3]};
+        else
+          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + obase + col) =
+              (u32x2){pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+      }
+    }
+}
+
 template <int KS, int MT, bool SL>
 int launch_f32(F32Params p, hipStream_t stream) {
   p.nqb = (p.N + 127) / 128;
@@ -622,6 +794,15 @@ int launch_f32(F32Params p, hipStream_t stream) {
                          stream, p);
       hipLaunchKernelGGL(f32_split_combine_kernel<MT>, dim3((unsigned)(p.nqb * 4 * MT), (unsigned)p.BH), dim3(256), 0,
                          stream, p);
+      return (int)hipGetLastError();
+    }
+  }
+  if constexpr (!SL && KS == 1 && MT <= 2) {
+    // grids that fill the CUs, 16-byte rows: three-term bf16 products on shared key tiles
+    if ((long long)p.nqb * p.BH >= device_cu_count() && p.vec && p.out_vec) {
+      constexpr int NW = 8;
+      p.nqb = (p.N + 32 * NW - 1) / (32 * NW);
+      hipLaunchKernelGGL((f32_x6_tiled_kernel<MT, NW>), dim3((unsigned)(p.nqb * p.BH)), dim3(64 * NW), 0, stream, p);
       return (int)hipGetLastError();
     }
   }
