@@ -243,10 +243,12 @@ def test_packed_work_group_sizes(B, H, N, dv):
 @pytest.mark.parametrize("B,H,N,d,dv", [(1, 4, 1024, 16, 64), (1, 1, 300, 16, 100), (1, 2, 1000, 32, 128),
                                         (2, 3, 257, 8, 24), (1, 1, 129, 4, 1)])
 def test_fp32_key_split(B, H, N, d, dv):
-    """fp32 inputs on small grids run every (query block, 64-key block) as its own work-group and
-    add the partial numerators and row sums in a second kernel: output, numerator and den against
-    fp64 (dv 100 and 128 the widest partials, dv 24 and 1 columns past dv in them; 300 and 257
-    tokens a ragged last query block, whose last key block may lie past N)."""
+    """fp32 inputs on small grids: shapes outside the three-term kernel (dv 100, 128, d 32, dv 1)
+    run every (query block, 64-key block) as its own work-group and add the partial numerators and
+    row sums in a second kernel; d <= 16, dv <= 64 with 16-byte rows (the first and fourth shapes)
+    run the three-term kernel.  Output, numerator and den against fp64 (dv 100 and 128 the widest
+    partials, dv 24 and 1 columns past dv in them; 300 and 257 tokens a ragged last query block,
+    whose last key block may lie past N)."""
     K = _kernels()
     L = _lib_mod().lib()
     need = L.la_based_parallel_workspace_bytes(B, H, N, d, dv, 0)
@@ -301,3 +303,20 @@ def test_fp32_small_grid_three_term_kernel(N, d, dv):
     assert rc == 0
     torch.cuda.synchronize()
     assert err(y2, want) < TOL_F32
+
+
+@pytest.mark.parametrize("B,H,N,dv", [(2, 64, 1024, 64), (1, 128, 1100, 32)])
+def test_fp32_large_grid_tiled_kernel(B, H, N, dv):
+    """fp32 grids whose 256-query blocks fill every CU twice run the tiled three-term kernel (key
+    tiles shared by 8 waves through LDS): output and den of a few heads against fp64, ragged N."""
+    K = _kernels()
+    d = 16
+    q, k, v = rand_qkv(B, H, N, d, dv, seed=N + H, dtype=torch.float32, scale_qk=1.0)
+    y, den = K.based_parallel(*to_dev(q, k, v), out_dtype=torch.float32, return_den=True)
+    y, den = y.cpu(), den.cpu()
+    for bb, hh in ((0, 0), (B - 1, H - 1), (0, H // 2)):
+        sl = (slice(bb, bb + 1), slice(hh, hh + 1))
+        want, _, want_den = ref.based_dense(q[sl], k[sl], v[sl])
+        e, ed = err(y[sl], want), err(den[sl], want_den)
+        print(f"tiled fp32 B{B} H{H} N{N} dv{dv} head ({bb},{hh}) err={e:.3e} den={ed:.3e}")
+        assert e < TOL_F32 and ed < TOL_F32

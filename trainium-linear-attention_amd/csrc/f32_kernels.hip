@@ -780,10 +780,17 @@ int launch_f32(F32Params p, hipStream_t stream) {
   p.nqb = (p.N + 127) / 128;
   const dim3 grid((unsigned)(p.nqb * p.BH));
   if constexpr (!SL && KS == 1 && MT <= 2) {
-    // small grids (the key-split condition) with 16-byte rows: three-term bf16 products, one launch
-    if (p.part != nullptr && p.vec && p.out_vec) {
-      p.nqb = (p.N + 31) / 32;
-      hipLaunchKernelGGL(f32_x6_kernel<MT>, dim3((unsigned)(p.nqb * p.BH)), dim3(512), 0, stream, p);
+    // d <= 16, dv <= 64 and 16-byte rows: three-term bf16 products.  Grids of 256-query blocks
+    // that fill every CU twice share each key tile among 8 waves (f32_x6_tiled_kernel); others
+    // run 32-query work-groups with the keys spread over 8 waves (f32_x6_kernel).
+    if (p.vec && p.out_vec) {
+      if ((long long)((p.N + 255) / 256) * p.BH >= 2LL * device_cu_count()) {
+        p.nqb = (p.N + 255) / 256;
+        hipLaunchKernelGGL((f32_x6_tiled_kernel<MT, 8>), dim3((unsigned)(p.nqb * p.BH)), dim3(512), 0, stream, p);
+      } else {
+        p.nqb = (p.N + 31) / 32;
+        hipLaunchKernelGGL(f32_x6_kernel<MT>, dim3((unsigned)(p.nqb * p.BH)), dim3(512), 0, stream, p);
+      }
       return (int)hipGetLastError();
     }
   }
@@ -794,15 +801,6 @@ int launch_f32(F32Params p, hipStream_t stream) {
                          stream, p);
       hipLaunchKernelGGL(f32_split_combine_kernel<MT>, dim3((unsigned)(p.nqb * 4 * MT), (unsigned)p.BH), dim3(256), 0,
                          stream, p);
-      return (int)hipGetLastError();
-    }
-  }
-  if constexpr (!SL && KS == 1 && MT <= 2) {
-    // grids that fill the CUs, 16-byte rows: three-term bf16 products on shared key tiles
-    if ((long long)p.nqb * p.BH >= device_cu_count() && p.vec && p.out_vec) {
-      constexpr int NW = 8;
-      p.nqb = (p.N + 32 * NW - 1) / (32 * NW);
-      hipLaunchKernelGGL((f32_x6_tiled_kernel<MT, NW>), dim3((unsigned)(p.nqb * p.BH)), dim3(64 * NW), 0, stream, p);
       return (int)hipGetLastError();
     }
   }
