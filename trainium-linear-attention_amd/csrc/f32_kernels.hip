@@ -560,47 +560,44 @@ __global__ __launch_bounds__(512) void f32_x6_kernel(const F32Params p) {
     tile(u);
   }
 
-  // wave-ordered sum of the numerators and row sums (the tables are free after the barrier)
+  // wave-ordered sum of the numerators and row sums (the tables are free after the barrier):
+  // every active wave parks its partial numerators as MT * 4 slices of four columns per lane
+  // and its row sums; wave s < 4 MT then adds slice s of all of them, in wave order, and stores
+  // its four columns of the outputs
+  constexpr int NSL = 4 * MT;
   const int nact = min(NW, ud + 1);
   float* red = reinterpret_cast<float*>(tabs);
   __syncthreads();
-  if (w > 0 && w < nact) {
+  if (w < nact) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) red[((w * MT + mt) * 16 + i) * 64 + lane] = acc[mt][i];
-    red[(NW * MT * 16 + w) * 64 + lane] = rsum;
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4*>(&red[((w * NSL + 4 * mt + g) * 64 + lane) * 4]) =
+            (f32x4){acc[mt][4 * g], acc[mt][4 * g + 1], acc[mt][4 * g + 2], acc[mt][4 * g + 3]};
+    red[NW * NSL * 256 + w * 64 + lane] = rsum;
   }
   __syncthreads();
-  if (w != 0) return;
-  for (int ww = 1; ww < nact; ++ww) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[mt][i] += red[((ww * MT + mt) * 16 + i) * 64 + lane];
-    rsum += red[(NW * MT * 16 + ww) * 64 + lane];
+  if (w >= NSL) return;
+  f32x4 y = {0.f, 0.f, 0.f, 0.f};
+  float rs = 0.f;
+  for (int ww = 0; ww < nact; ++ww) {
+    y += *reinterpret_cast<const f32x4*>(&red[((ww * NSL + w) * 64 + lane) * 4]);
+    rs += red[NW * NSL * 256 + ww * 64 + lane];
   }
-  const float rs = rsum + __shfl_xor(rsum, 32);
+  rs += __shfl_xor(rs, 32);
   if (query >= N) return;
   const float inv = p.normalize ? 1.0f / (rs + p.eps) : 1.0f;
-  if (p.den != nullptr && h == 0) p.den[hrow + query] = rs;
+  if (p.den != nullptr && w == 0 && h == 0) p.den[hrow + query] = rs;
   const size_t obase = (hrow + query) * (size_t)dv;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int col = 32 * mt + 8 * g + 4 * h;
-      float y[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = acc[mt][4 * g + e] * inv;
-      if (col < dv) {
-        if (p.out_f32)
-          *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + obase + col) = (f32x4){y[0], y[1], y[2], y[3]};
-        else
-          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + obase + col) =
-              (u32x2){pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
-      }
-    }
+  const int col = 32 * (w >> 2) + 8 * (w & 3) + 4 * h;
+  if (col < dv) {
+    if (p.out_f32)
+      *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + obase + col) = (f32x4){y[0] * inv, y[1] * inv, y[2] * inv, y[3] * inv};
+    else
+      *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + obase + col) =
+          (u32x2){pack_bf16x2(y[0] * inv, y[1] * inv), pack_bf16x2(y[2] * inv, y[3] * inv)};
+  }
 }
 
 // fp32 BASED on larger grids, with the three-term bf16 products of f32_x6_kernel: work-group
