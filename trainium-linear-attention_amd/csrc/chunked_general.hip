@@ -7,8 +7,8 @@
 //
 // Kernel 0 (gprep_kernel) converts every 64-token chunk before the last segment once: per-token
 // normalised fp16 k~^T rows, v n^2 rows and the n^2 row with the chunk's exponents.
-// Kernel 1 (gstate_kernel): one work-group per (head, 16 groups); its four waves hold two
-// 32-feature tiles each as fp32 MFMA accumulators over dv and sweep the head's converted chunks
+// Kernel 1 (gstate_kernel): one work-group per (head, 16 groups); its eight waves hold one
+// 32-feature tile each as fp32 MFMA accumulators over dv and sweep the head's converted chunks
 // through an LDS ring (buffer_load ... lds, NS - 1 chunks ahead): A = feature rows (one
 // v_pk_mul_f16 per two products k~_i k~_j), B = the V^T rows, K = tokens, fp16 MFMAs; z from the
 // same products against the n^2 row.  After every segment but the last it writes the state so
@@ -195,16 +195,24 @@ __global__ __launch_bounds__(256) void gprep_kernel(const GParams p) {
 // ---------------------------------------------------------------- kernel 1: segment states
 // Sequences with few heads split the sweep into p.nparts parts of p.spp segments: a TOTAL pass
 // sums every part but the last (no prefixes written), then each part's work-group starts from
-// the totals of the parts before it and writes its segments' prefixes.
-template <int DP, int DVT, bool TOTAL>
-__global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
+// the totals of the parts before it and writes its segments' prefixes.  The work-group's eight
+// 32-feature tiles go to 8 / TW waves of TW tiles each.
+template <int DP, int DVT, bool TOTAL, int TW>
+__global__ __launch_bounds__(64 * (8 / TW), TW == 1 ? 4 : 1) void gstate_kernel(const GParams p) {
   using FT = GFeat<DP>;
   using CK = GChunk<DP, DVT>;
+  constexpr int NWV = 8 / TW, NT = 64 * NWV;
   constexpr int DVP = CK::DVP, NS = DVT == 4 ? 3 : 4;   // ring stages (prefetch distance NS - 1)
   // a stage: the chunk's rows, then 16 zero rows standing for k~^T rows DP + 1 .. DP + 16
   constexpr int SH = CK::HALVES + 16 * GC;
   __shared__ __attribute__((aligned(16))) uint16_t ring[NS][SH];
-  __shared__ u32 red[3][4];
+  __shared__ u32 red[3][NWV];
+  auto red_max = [&](int row) {
+    u32 m = red[row][0];
+#pragma unroll
+    for (int i = 1; i < NWV; ++i) m = max(m, red[row][i]);
+    return m;
+  };
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
   const int nwga = FT::NWGA;
@@ -225,15 +233,15 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
   const int nch = (p.nseg - 1) * (GL / GC);
   const int cps = GL / GC;
   const int c0 = part * p.spp * cps, c1 = min((part + 1) * p.spp, p.nseg - 1) * cps;   // this part's chunks
-  constexpr int PER = 2 * DVT * 16 + 2;   // a thread's sums: accumulators, then z partials
+  constexpr int PER = TW * (DVT * 16 + 1);   // a thread's sums: accumulators, then z partials
   const uint16_t* __restrict__ src = p.KV + (size_t)bh * nch * CK::HALVES;
   const u32x2* __restrict__ ce = p.CE + (size_t)bh * nch;
 
-  for (int x = tid; x < NS * 16 * GC; x += 256) ring[x / (16 * GC)][CK::HALVES + x % (16 * GC)] = 0;
+  for (int x = tid; x < NS * 16 * GC; x += NT) ring[x / (16 * GC)][CK::HALVES + x % (16 * GC)] = 0;
 
   // the head's reference exponents: the largest chunk exponents
   u32 mc = 0u, mz = 0u;   // biased by 1024 so that the unsigned maximum orders them
-  for (int c = tid; c < nch; c += 256) {
+  for (int c = tid; c < nch; c += NT) {
     const u32x2 e2 = ce[c];
     mc = max(mc, (u32)((int)e2[0] + 1024));
     mz = max(mz, (u32)((int)e2[1] + 1024));
@@ -245,13 +253,13 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
     red[1][w] = mz;
   }
 
-  // this lane's feature rows of its two tiles: k~^T row i (<= DP) and row j (> DP: a zero row of
+  // this lane's feature rows of its tiles: k~^T row i (<= DP) and row j (> DP: a zero row of
   // the stage).  A wave whose tile lies past the last one computes group 0 and stores nothing.
-  int ri[2], rj[2], xi[2], xj[2];
-  bool tv[2];
+  int ri[TW], rj[TW], xi[TW], xj[TW];
+  bool tv[TW];
 #pragma unroll
-  for (int mw = 0; mw < 2; ++mw) {
-    const int tt = 8 * wga + 2 * w + mw;
+  for (int mw = 0; mw < TW; ++mw) {
+    const int tt = 8 * wga + TW * w + mw;
     tv[mw] = tt < FT::NT;
     int i, J;
     group_ij<DP>(tv[mw] ? 2 * tt + (n >> 4) : 0, i, J);
@@ -265,41 +273,43 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
 #pragma unroll
   for (int nt = 0; nt < DVT; ++nt) rv[nt] = CK::RV + 32 * nt + n;
 
-  constexpr int UW = (CK::UNITS + 3) / 4;   // most copy units per wave and chunk
-  const int my_units = CK::UNITS / 4 + (w < CK::UNITS % 4 ? 1 : 0);
+  constexpr int UW = (CK::UNITS + NWV - 1) / NWV;   // most copy units per wave and chunk
+  const int my_units = CK::UNITS / NWV + (w < CK::UNITS % NWV ? 1 : 0);
   const u32x4 rsrc = buffer_rsrc(src, (u32)((size_t)nch * CK::HALVES * 2));
   auto issue = [&](int c) {
     if (c >= c1) return;
     const u32 base = lds_addr(&ring[c % NS][0]);
 #pragma unroll
     for (int x = 0; x < UW; ++x) {
-      const int u = w + 4 * x;
+      const int u = w + NWV * x;
       if (u < CK::UNITS) lds_copy16(rsrc, base + 1024 * u, c * (CK::HALVES * 2) + 1024 * u + 16 * lane);
     }
   };
   __syncthreads();
-  const int eref = (int)max(max(red[0][0], red[0][1]), max(red[0][2], red[0][3])) - 1024;
-  const int ezref = (int)max(max(red[1][0], red[1][1]), max(red[1][2], red[1][3])) - 1024;
+  const int eref = (int)red_max(0) - 1024;
+  const int ezref = (int)red_max(1) - 1024;
 
-  f32x16 acc[2][DVT];
-  float zc[2] = {0.f, 0.f};
+  f32x16 acc[TW][DVT];
+  float zc[TW];
 #pragma unroll
-  for (int mw = 0; mw < 2; ++mw)
+  for (int mw = 0; mw < TW; ++mw) zc[mw] = 0.f;
+#pragma unroll
+  for (int mw = 0; mw < TW; ++mw)
 #pragma unroll
     for (int nt = 0; nt < DVT; ++nt) acc[mw][nt] = splat16(0.f);
 
   if (!TOTAL) {
     // the parts before this one
     for (int q = 0; q < part; ++q) {
-      const float* t = p.Tot + (((size_t)q * p.BH + bh) * nwga + wga) * (256 * PER) + tid * PER;
+      const float* t = p.Tot + (((size_t)q * p.BH + bh) * nwga + wga) * (NT * PER) + tid * PER;
 #pragma unroll
-      for (int mw = 0; mw < 2; ++mw)
+      for (int mw = 0; mw < TW; ++mw) {
 #pragma unroll
         for (int nt = 0; nt < DVT; ++nt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[mw][nt][r] += t[(mw * DVT + nt) * 16 + r];
-      zc[0] += t[PER - 2];
-      zc[1] += t[PER - 1];
+        zc[mw] += t[TW * DVT * 16 + mw];
+      }
     }
   }
   for (int c = c0; c < c0 + NS - 1; ++c) issue(c);
@@ -331,14 +341,14 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
       if (sc)
 #pragma unroll
         for (int c4 = 0; c4 < 4; ++c4) nz[c4] = pk_mul_f16(nz[c4], fzp);
-      u32x4 bi[2], bj[2];
+      u32x4 bi[TW], bj[TW];
 #pragma unroll
-      for (int mw = 0; mw < 2; ++mw) {
+      for (int mw = 0; mw < TW; ++mw) {
         bi[mw] = *reinterpret_cast<const u32x4*>(st + ri[mw] * GC + ((u ^ xi[mw]) << 3));
         bj[mw] = *reinterpret_cast<const u32x4*>(st + rj[mw] * GC + ((u ^ xj[mw]) << 3));
       }
 #pragma unroll
-      for (int mw = 0; mw < 2; ++mw) {
+      for (int mw = 0; mw < TW; ++mw) {
         const u32x4 af = {pk_mul_f16(bi[mw][0], bj[mw][0]), pk_mul_f16(bi[mw][1], bj[mw][1]),
                           pk_mul_f16(bi[mw][2], bj[mw][2]), pk_mul_f16(bi[mw][3], bj[mw][3])};
 #pragma unroll
@@ -348,10 +358,10 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
       }
     };
     if (scaled) {
-#pragma unroll
+#pragma unroll 1
       for (int ks = 0; ks < GC / 16; ++ks) kstep(ks, true);
     } else {
-#pragma unroll
+#pragma unroll 1
       for (int ks = 0; ks < GC / 16; ++ks) kstep(ks, false);
     }
 
@@ -360,10 +370,10 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
       // T 2^-eref, zc z 2^-ezref; the slot's exponent E puts the largest of both in
       // [2^13, 2^14).
       const int s = gc / cps;
-      float zz[2];
+      float zz[TW];
       u32 ma = 0u, mzz = 0u;
 #pragma unroll
-      for (int mw = 0; mw < 2; ++mw) {
+      for (int mw = 0; mw < TW; ++mw) {
         zz[mw] = zc[mw] + __shfl_xor(zc[mw], 32);
         if (!tv[mw]) continue;
         mzz = max(mzz, __builtin_bit_cast(u32, __builtin_fabsf(zz[mw])));
@@ -379,8 +389,8 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
         red[2][w] = mzz;
       }
       __syncthreads();
-      ma = max(max(red[0][0], red[0][1]), max(red[0][2], red[0][3]));
-      mzz = max(max(red[2][0], red[2][1]), max(red[2][2], red[2][3]));
+      ma = red_max(0);
+      mzz = red_max(2);
       const int ea = ma == 0u ? -1000 : (int)(ma >> 23) - 127 + eref;
       const int ez = mzz == 0u ? -1000 : (int)(mzz >> 23) - 127 + ezref;
       const int E = max(max(ea, ez) - 13, -100);
@@ -389,9 +399,9 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
       uint16_t* Ts = p.T + slot * (size_t)(FT::NGB * DVP * 64);
       uint16_t* Zs = p.Z + slot * (size_t)(FT::NGB * 64);
 #pragma unroll
-      for (int mw = 0; mw < 2; ++mw) {
+      for (int mw = 0; mw < TW; ++mw) {
         if (!tv[mw]) continue;
-        const int tt = 8 * wga + 2 * w + mw;
+        const int tt = 8 * wga + TW * w + mw;
 #pragma unroll
         for (int nt = 0; nt < DVT; ++nt) {
           const int row = 32 * nt + n;
@@ -413,15 +423,15 @@ __global__ __launch_bounds__(256) void gstate_kernel(const GParams p) {
     }
   }
   if (TOTAL) {
-    float* t = p.Tot + (((size_t)part * p.BH + bh) * nwga + wga) * (256 * PER) + tid * PER;
+    float* t = p.Tot + (((size_t)part * p.BH + bh) * nwga + wga) * (NT * PER) + tid * PER;
 #pragma unroll
-    for (int mw = 0; mw < 2; ++mw)
+    for (int mw = 0; mw < TW; ++mw) {
 #pragma unroll
       for (int nt = 0; nt < DVT; ++nt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) t[(mw * DVT + nt) * 16 + r] = acc[mw][nt][r];
-    t[PER - 2] = zc[0];
-    t[PER - 1] = zc[1];
+      t[TW * DVT * 16 + mw] = zc[mw];
+    }
   }
 }
 
@@ -737,7 +747,9 @@ GLayout glayout_dp(int BH, int nseg, int DVT) {
   L.ce = L.kv + up(nchk * halves * 2);
   L.tot = L.ce + up(nchk * 8);
   state_parts(BH, FT::NWGA, nseg, L.nparts, L.spp);
-  L.total = L.tot + up((size_t)(L.nparts - 1) * BH * FT::NWGA * 256 * (2 * DVT * 16 + 2) * 4);
+  // per state work-group of every part but the last: its eight tiles' sums, 32 x DVT accumulators
+  // and a z partial per lane
+  L.total = L.tot + up((size_t)(L.nparts - 1) * BH * FT::NWGA * 512 * (DVT * 16 + 1) * 4);
   return L;
 }
 
@@ -751,6 +763,11 @@ GLayout glayout(int BH, int N, int d, int dv) {
   }
 }
 
+// 32-feature tiles per wave of the state kernel: one (8 waves of at most 128 VGPRs, two
+// work-groups per CU) up to dv = 64; two (4 waves) for dv = 128, whose accumulators need more
+template <int DVT>
+constexpr int state_tw() { return DVT == 4 ? 2 : 1; }
+
 template <int DP, int DVT>
 int launch_g(const GParams& p, hipStream_t stream) {
   using FT = GFeat<DP>;
@@ -761,12 +778,13 @@ int launch_g(const GParams& p, hipStream_t stream) {
     if (e != 0) return e;
     const unsigned units = (unsigned)(p.BH * FT::NWGA);
     if (p.nparts > 1) {
-      hipLaunchKernelGGL((gstate_kernel<DP, DVT, true>), dim3(units * (unsigned)(p.nparts - 1)), dim3(256), 0, stream,
-                         p);
+      hipLaunchKernelGGL((gstate_kernel<DP, DVT, true, state_tw<DVT>()>), dim3(units * (unsigned)(p.nparts - 1)),
+                         dim3(64 * (8 / state_tw<DVT>())), 0, stream, p);
       e = (int)hipGetLastError();
       if (e != 0) return e;
     }
-    hipLaunchKernelGGL((gstate_kernel<DP, DVT, false>), dim3(units * (unsigned)p.nparts), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((gstate_kernel<DP, DVT, false, state_tw<DVT>()>), dim3(units * (unsigned)p.nparts),
+                       dim3(64 * (8 / state_tw<DVT>())), 0, stream, p);
     e = (int)hipGetLastError();
     if (e != 0) return e;
   }
