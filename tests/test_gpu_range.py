@@ -8,6 +8,8 @@ bf16 inputs of any magnitude the reference's own bf16 arithmetic handles
 call, blocks of one head on both sides of the kernels' scale steps, scores s = q.k/sqrt(d) up to
 about 300, a mean-biased V over 65536 tokens (its sums grow linearly with N), the long-context
 configuration without pre-scaling, and a continuation from a state with a large sum of v.
+The fp32 inputs that run as three bf16 terms per operand are held to the fp32 bar for V scaled
+by 1e30 and 1e-30 and for large scores.
 """
 
 import pytest
@@ -168,3 +170,24 @@ def test_continue_from_large_state():
             e = max(e, ref.rel_err(y2[0, h, r0:r0 + 32], rows_fp64(q, k, v, 0, h, rows)))
     print(f"continuation from a large state: rows err={e:.3e}")
     assert e < TOL
+
+
+TOL_F32 = 1e-4
+
+
+@pytest.mark.parametrize("vscale,qk", [(1e30, 1.0), (1e-30, 1.0), (1.0, 8.0)])
+@pytest.mark.parametrize("B,H,N", [(1, 3, 777), (2, 64, 1024)])
+def test_fp32_three_term_range(vscale, qk, B, H, N):
+    """fp32 inputs on the kernels that split every operand into three bf16 terms (the small-grid
+    kernel at B1 H3, the tiled one at B2 H64): V scaled by 1e30 and 1e-30 (terms of magnitude
+    |v|, |v| 2^-8 and |v| 2^-16, all inside bf16's normal range) and scores up to about 300, at
+    the fp32 bar against fp64 on the first and last heads."""
+    q, k, v = rand_qkv(B, H, N, 16, 64, seed=N + H, dtype=torch.float32, scale_qk=qk)
+    v = v * vscale
+    y = _kernels().based_parallel(*to_dev(q, k, v), out_dtype=torch.float32).cpu()
+    for bb, hh in ((0, 0), (B - 1, H - 1)):
+        sl = (slice(bb, bb + 1), slice(hh, hh + 1))
+        want, _, _ = ref.based_dense(q[sl], k[sl], v[sl])
+        e = err(y[sl], want)
+        print(f"fp32 three-term B{B} H{H} N{N} v x {vscale:g} qk x {qk:g} head ({bb},{hh}): err={e:.3e}")
+        assert e < TOL_F32
