@@ -9,7 +9,8 @@ call, blocks of one head on both sides of the kernels' scale steps, scores s = q
 about 300, a mean-biased V over 65536 tokens (its sums grow linearly with N), the long-context
 configuration without pre-scaling, and a continuation from a state with a large sum of v.
 The fp32 inputs that run as three bf16 terms per operand are held to the fp32 bar for V scaled
-by 1e30 and 1e-30 and for large scores.
+by 1e30 and 1e-30 and for large scores, and the sliding-window softmax (resident and streaming
+kernels) to the bf16 bar for the same V scales and scores of several hundred.
 """
 
 import pytest
@@ -191,3 +192,19 @@ def test_fp32_three_term_range(vscale, qk, B, H, N):
         e = err(y[sl], want)
         print(f"fp32 three-term B{B} H{H} N{N} v x {vscale:g} qk x {qk:g} head ({bb},{hh}): err={e:.3e}")
         assert e < TOL_F32
+
+
+@pytest.mark.parametrize("vscale,qk", [(1e30, 1.0), (1e-30, 1.0), (1.0, 20.0)])
+@pytest.mark.parametrize("W", [64, 200])
+def test_sliding_range(vscale, qk, W):
+    """bf16 sliding-window softmax (the resident kernel at W = 64, the streaming one at W = 200)
+    for V far from 1 (the P.V products run on bf16 MFMAs with P split into hi + lo, so V keeps
+    bf16's range) and scores of several hundred (softmax in fp32 against the running maximum):
+    fp32 output against fp64 at the bf16 bar."""
+    q, k, v = _scaled(1, 2, 1000, 64, 64, seed=W + 7, vscale=vscale, qk=qk)
+    K = _kernels()
+    y = K.sliding_window_attn(*to_dev(q, k, v), window_size=W, out_dtype=torch.float32)
+    want = ref.sliding_dense(q, k, v, window_size=W)
+    e = max(head_errs(y, want))
+    print(f"sliding W={W} v x {vscale:g} qk x {qk:g}: err={e:.3e}")
+    assert torch.isfinite(y).all() and e < TOL
