@@ -357,11 +357,13 @@ __global__ __launch_bounds__(64 * (8 / TW), TW == 1 ? 4 : 1) void gstate_kernel(
         for (int nt = 0; nt < DVT; ++nt) acc[mw][nt] = mfma32x32x16_f16(af, vf[nt], acc[mw][nt]);
       }
     };
+    // one K step at a time on one-tile waves (the 128-VGPR budget), all of them unrolled on two
+    constexpr int KSU = TW == 1 ? 1 : GC / 16;
     if (scaled) {
-#pragma unroll 1
+#pragma unroll KSU
       for (int ks = 0; ks < GC / 16; ++ks) kstep(ks, true);
     } else {
-#pragma unroll 1
+#pragma unroll KSU
       for (int ks = 0; ks < GC / 16; ++ks) kstep(ks, false);
     }
 
