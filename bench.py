@@ -560,8 +560,8 @@ def main():
     args = parse()
     SETTLE_MS = args.settle_ms
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the multi-GPU sharding is described in "
-              "DESIGN.md and not launched", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); how the path would shard over several "
+              "GPUs is a design, not a launched path", file=sys.stderr)
         sys.exit(2)
     import torch
 
