@@ -228,7 +228,9 @@ def measure(cfg, steps, warmup, rotate, device, main_only=False):
     name, kind, B, H, N, d, dv, dt, seed, chunk, window, prescale = cfg
     esz = 2 if dt == "bf16" else 4
     crun = chunk_run(chunk) if kind == "chunked" else chunk
-    flop, nbytes = work(kind, B, H, N, d, dv, esz, crun, window)
+    # algorithmic work at the chunk size the configuration states (the recurrence computes the
+    # same function at any chunk size; the chunk the kernels run is reported beside it)
+    flop, nbytes = work(kind, B, H, N, d, dv, esz, chunk, window)
     hbm_bound = kind != "parallel"
     nsets = rotate if hbm_bound else 1
     calls = []
@@ -254,7 +256,7 @@ def measure(cfg, steps, warmup, rotate, device, main_only=False):
         "input_sets": nsets,
     }
     if kind == "chunked":
-        res["tflops_f153"] = round(B * H * N * (4 * feature_dim(d) * dv + (crun + 1) * (d + dv)) / sec / 1e12, 3)
+        res["tflops_f153"] = round(B * H * N * (4 * feature_dim(d) * dv + (chunk + 1) * (d + dv)) / sec / 1e12, 3)
     del calls
     torch_empty_cache()
     return res
@@ -463,6 +465,29 @@ def torch_empty_cache():
     torch.cuda.empty_cache()
 
 
+def cpu_threads():
+    """Threads for the CPU baseline and a description of the host CPU.  A job on a shared host
+    is given its share of the cores in OMP_NUM_THREADS, while its affinity mask may show more
+    cores than that share.  So: every core of the affinity mask, capped by OMP_NUM_THREADS when
+    it is set."""
+    aff = len(os.sched_getaffinity(0))
+    threads = aff
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        threads = min(threads, int(env))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return max(1, threads), {"cpu_model": model, "affinity_cores": aff,
+                             "omp_num_threads": env or None}
+
+
 def cpu_baseline(chunk_heads, min_seconds=10.0):
     """The oracle's restatement of the reference PyTorch path (kernels/pytorch_attention.py:27-42,
     computed in bf16 as the reference does) over the whole headline workload -- all B*H heads,
@@ -472,7 +497,7 @@ def cpu_baseline(chunk_heads, min_seconds=10.0):
 
     from oracle import reference as ref
 
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    threads, host = cpu_threads()
     torch.set_num_threads(threads)
     _, _, B, H, N, d, dv, dt, seed, _, _, prescale = HEADLINE
     q, k, v = make_inputs(B, H, N, d, dv, dt, seed, prescale, "cpu")
@@ -497,6 +522,7 @@ def cpu_baseline(chunk_heads, min_seconds=10.0):
                   f"restated reference ref_based_attn (kernels/pytorch_attention.py:27-42) in bf16 on CPU, "
                   f"{passes} passes in {sec:.1f} s ({sec / passes:.2f} s per pass)",
         "sample_seconds": round(sec, 3),
+        **host,
     }
 
 
@@ -516,7 +542,7 @@ def cpu_config_baseline(cfg, budget_s=3.0):
     from oracle import reference as ref
 
     name, kind, B, H, N, d, dv, dt, seed, chunk, window, prescale = cfg
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    threads, host = cpu_threads()
     torch.set_num_threads(threads)
     q, k, v = make_inputs(B, H, N, d, dv, dt, seed, prescale, "cpu")
     q, k, v = (x.reshape(1, B * H, N, x.shape[-1]) for x in (q, k, v))
@@ -544,7 +570,7 @@ def cpu_config_baseline(cfg, budget_s=3.0):
     ms = sec / heads * B * H * 1e3
     return {"ms": round(ms, 3), "cores": threads, "kind": "port",
             "sample": f"{what}, {heads} head evaluations of {B * H} heads in {sec:.2f} s after one warm-up head, "
-                      f"scaled to all heads"}
+                      f"scaled to all heads", **host}
 
 
 def load_traffic(kernel):
