@@ -1101,13 +1101,16 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
     }
 
     // ---- intra-chunk: key tiles j <= W; scores b/2 = 1/2 + q~.(k~/2), P = (b/2)^2 + 1/4 = p/2.
-    // The call's first chunk also takes P's fp16 remainder lo = fp16(P - hi) through a second P.V
-    // MFMA: without an initial state its first rows' outputs are single tokens' v, far above the
-    // head's rms (what the parity metric divides by), and hi + lo keeps ~22 bits of P; later rows
-    // average enough keys that fp16 P alone is well inside the bar.  (Taken with an initial state
-    // too, so that a zero state gives the plain call's result; vector-path kernels only: the
-    // scalar-store kernel has no registers to spare for it.)
-    const bool exact = VEC && row0 == 0;
+    // The call's first 64 queries (waves 0 and 1 of its first chunk) also take P's fp16 remainder
+    // lo = fp16(P - fp16(P)) through a second P.V MFMA: without an initial state these rows'
+    // outputs average a few tokens' v, far above the head's rms (what the parity metric divides
+    // by), and hi + lo keeps ~22 bits of P; later rows average enough keys that fp16 P alone is
+    // well inside the bar (worst head of B2 H16 N8192: 2.1e-2 without these rows, 3.7e-3 with
+    // them; of B1 H16 N65536: 8.7e-3 with them).
+    // Taken with an initial state too, so that a zero state gives the plain call's result; only
+    // in waves 0 and 1 of the vector-path kernels, whose loops carry the extra code without
+    // spilling or slowing down.
+    const bool exact = W <= 1 && VEC && !LAYER && row0 == 0;
     float rs = 0.f;
 #pragma unroll
     for (int j = 0; j <= W; ++j) {
@@ -1124,7 +1127,7 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
           pl[x] &= dmask[x];
         }
         rs = dot2_f16(pk[x], kOnes, rs);
-        rs = dot2_f16(pl[x], kOnes, rs);
+        if (exact) rs = dot2_f16(pl[x], kOnes, rs);
       }
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
