@@ -159,8 +159,12 @@ int la_based_chunked_fwd_continue(const void* q, const void* k, const void* v, i
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
  * No counterpart in the reference.  The kernels' scratch is a fixed device array of
  * LA_NOALLOC_SCRATCH_BYTES inside the library (one per device, held until the process ends);
- * shapes that would need more return LA_ERR_SCRATCH_LIMIT (32 MiB covers every shape: at most
- * about 1022 (head, segment) records of 24 KiB are used).  The call allocates nothing.  Calls
+ * shapes that would need more return LA_ERR_SCRATCH_LIMIT before touching the device.  For bf16
+ * d = 16, dv <= 64 (the chunk recurrence) 32 MiB covers every shape: at most about 1022 (head,
+ * segment) records of 24 KiB are used.  The segment-state path (other d, dv > 64, fp32 inputs)
+ * keeps state prefixes per (head, 512-token segment), which grow with B*H*N: e.g. bf16 B2 H16
+ * N8192 d64 needs 224 MiB and is refused (la_based_chunked_workspace_bytes_dt gives the need).
+ * The call allocates nothing.  Calls
  * that overlap in time on one device share the array and race: serialise them (one stream, or
  * the caller's own ordering).  Other arguments, limits and results as la_based_chunked_fwd.
  */
@@ -202,8 +206,8 @@ int la_sliding_window_fwd_add(const void* q, const void* k, const void* v, int i
  * la_sliding_window_fwd's (scale_sw, window); after the chunked state passes one kernel computes
  * both branches per (head, segment) and stores their sum, rounded once to out_dtype.
  * q, k: (B,H,N,16); q_sw, k_sw: (B,H,N,d_sw); v, out: (B,H,N,dv); all bf16 inputs, every
- * tensor 16-byte aligned.  workspace: la_based_chunked_workspace_bytes(B, H, N, 16, dv, 64)
- * bytes, 16-byte aligned.  Limits: d = 16, dv % 8 == 0 and dv <= 64, d_sw in {16, 32, 64},
+ * tensor 16-byte aligned.  workspace: la_based_chunked_workspace_bytes_dt(B, H, N, 16, dv, 64,
+ * LA_BF16) bytes, 16-byte aligned.  Limits: d = 16, dv % 8 == 0 and dv <= 64, d_sw in {16, 32, 64},
  * 1 <= window <= 64 (LA_ERR_UNSUPPORTED_DIM otherwise; such layers are the two calls).
  */
 int la_based_layer_fwd(const void* q, const void* k, const void* v, const void* q_sw, const void* k_sw,

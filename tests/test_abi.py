@@ -332,6 +332,11 @@ def test_chunked_noalloc_argument_errors():
     assert call(dt=5) == -3
     # largest scratch need below the limit: 511 heads x 2 segments of 24 KiB records
     assert lib.la_based_chunked_workspace_bytes_dt(1, 511, 256, 16, 64, 64, 1) <= (32 << 20)
+    # the segment-state path (d != 16, fp32) needs scratch that grows with B*H*N: refused above
+    # the fixed array, before the device is touched
+    assert lib.la_based_chunked_workspace_bytes_dt(2, 16, 8192, 64, 64, 64, 1) > (32 << 20)
+    assert call(d=64, dv=64, B=2, H=16, N=8192) == -10
+    assert call(d=16, dv=64, B=8, H=16, N=65536, dt=0) == -10
 
 
 def test_lds_copy_carries_its_wait_states():

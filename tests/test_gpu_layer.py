@@ -94,7 +94,7 @@ def _fused(q, k, v, q_sw, k_sw, W, out_dtype):
     b, h, t, d = q.shape
     dv, d_sw = v.shape[-1], q_sw.shape[-1]
     out = torch.empty(b, h, t, dv, dtype=out_dtype, device="cuda")
-    nb = int(L.la_based_chunked_workspace_bytes(b, h, t, d, dv, 64))
+    nb = int(L.la_based_chunked_workspace_bytes_dt(b, h, t, d, dv, 64, 1))
     ws = torch.empty(max(nb, 16), dtype=torch.uint8, device="cuda")
     rc = L.la_based_layer_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), q_sw.data_ptr(), k_sw.data_ptr(),
                               _lib.dtype_code(q.dtype), out.data_ptr(), _lib.dtype_code(out_dtype), b, h, t, d, dv,

@@ -208,3 +208,18 @@ def test_sliding_range(vscale, qk, W):
     e = max(head_errs(y, want))
     print(f"sliding W={W} v x {vscale:g} qk x {qk:g}: err={e:.3e}")
     assert torch.isfinite(y).all() and e < TOL
+
+
+def test_general_zero_key_dims_large_v():
+    """Segment-state path (d = 64): keys zero in dims 16..63 over the first 512-token segment, so
+    the work-groups of feature groups built from those dims see an all-zero state prefix (stored
+    as zeros, whatever scale the slot's other part sets), with V scaled by 1e10: finite outputs
+    at the bf16 bar against fp64."""
+    q, k, v = _scaled(1, 2, 1500, 64, 64, seed=18, vscale=1e10, qk=0.5)
+    k = k.clone()
+    k[:, :, :512, 16:] = 0
+    want, _, _ = ref.based_dense(q, k, v)
+    y = _run("chunked", q, k, v)
+    errs = head_errs(y, want)
+    print(f"general d64 zero key dims, v x 1e10: errs " + " ".join(f"{x:.2e}" for x in errs))
+    assert torch.isfinite(y).all() and max(errs) < TOL

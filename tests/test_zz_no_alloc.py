@@ -1,7 +1,8 @@
 """The no-allocation chunked entry point (la_based_chunked_fwd_noalloc) against la_based_chunked_fwd
 through the C ABI: two calls in a row on one device, the second with a smaller input, each bit
 for bit equal to the workspace entry point's output and exported state (the same kernels run on
-the same inputs; only the scratch memory differs)."""
+the same inputs; only the scratch memory differs) -- for the d = 16 recurrence and for shapes of
+the segment-state path (d = 64 bf16, fp32 inputs) whose scratch fits the fixed array."""
 
 import os
 import sys
@@ -51,3 +52,31 @@ def test_noalloc_matches_workspace_entry_point(shapes):
         torch.cuda.synchronize()
         assert torch.equal(got, want), (got - want).abs().max().item()
         assert torch.equal(got_s, want_s), (got_s - want_s).abs().max().item()
+
+
+def _general_pair(L, dt, B, H, N, d, dv, seed):
+    torch_dt = torch.bfloat16 if dt == 1 else torch.float32
+    q, k, v = (x.cuda() for x in rand_qkv(B, H, N, d, dv, seed, torch_dt, scale_qk=0.5))
+    stream = torch.cuda.current_stream().cuda_stream
+    nb = int(L.la_based_chunked_workspace_bytes_dt(B, H, N, d, dv, 64, dt))
+    assert 0 < nb <= (32 << 20), nb
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    want = torch.empty(B, H, N, dv, dtype=torch.float32, device="cuda")
+    got = torch.full_like(want, float("nan"))
+    scale = 1.0 / d ** 0.5
+    assert L.la_based_chunked_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, want.data_ptr(), 0, B, H, N, d, dv,
+                                  64, scale, 1e-6, 1, ws.data_ptr(), nb, None, stream) == 0
+    assert L.la_based_chunked_fwd_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, got.data_ptr(), 0, B, H, N,
+                                          d, dv, 64, scale, 1e-6, 1, None, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), (got - want).abs().max().item()
+
+
+@pytest.mark.parametrize("dt,shapes", [(1, ((1, 4, 3000, 64, 64), (1, 2, 1100, 64, 48))),
+                                       (0, ((2, 4, 3000, 16, 64), (1, 3, 1200, 16, 32)))])
+def test_noalloc_segment_state_path(dt, shapes):
+    from kernels import _lib
+    L = _lib.lib()
+    for i, (B, H, N, d, dv) in enumerate(shapes):
+        print(f"noalloc segment-state call {i}: dtype {dt} B{B} H{H} N{N} d{d} dv{dv}", flush=True)
+        _general_pair(L, dt, B, H, N, d, dv, 50 + i)

@@ -1119,9 +1119,13 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
       u32 pk[8], pl[8];
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
-        const float pa = __builtin_fmaf(sc[2 * x], sc[2 * x], 0.25f), pb = __builtin_fmaf(sc[2 * x + 1], sc[2 * x + 1], 0.25f);
-        pk[x] = pack_f16x2(pa, pb);
-        pl[x] = exact ? pack_f16x2(pa - f16_lo_to_f32(pk[x]), pb - f16_hi_to_f32(pk[x])) : 0u;
+        pk[x] = sq_plus_f16x2(sc[2 * x], sc[2 * x + 1], 0.25f);
+        if (exact) {
+          const float pa = __builtin_fmaf(sc[2 * x], sc[2 * x], 0.25f), pb = __builtin_fmaf(sc[2 * x + 1], sc[2 * x + 1], 0.25f);
+          pl[x] = pack_f16x2(pa - f16_lo_to_f32(pk[x]), pb - f16_hi_to_f32(pk[x]));
+        } else {
+          pl[x] = 0u;
+        }
         if (j == W) {
           pk[x] &= dmask[x];
           pl[x] &= dmask[x];

@@ -396,7 +396,11 @@ __global__ __launch_bounds__(64 * (8 / TW), TW == 1 ? 4 : 1) void gstate_kernel(
       const int ea = ma == 0u ? -1000 : (int)(ma >> 23) - 127 + eref;
       const int ez = mzz == 0u ? -1000 : (int)(mzz >> 23) - 127 + ezref;
       const int E = max(max(ea, ez) - 13, -100);
-      const float sc = __builtin_ldexpf(1.0f, eref - E), scz = __builtin_ldexpf(1.0f, ezref - E);
+      // an all-zero part is stored as zeros (its scale could exceed fp32 when the other part
+      // sets E, and 0 * inf would be NaN); a nonzero part's scale is at most 2^127, since
+      // E >= its own exponent - 13 (values below 2^-114 of the slot's largest then flush)
+      const float sc = ma == 0u ? 0.f : __builtin_ldexpf(1.0f, min(eref - E, 127));
+      const float scz = mzz == 0u ? 0.f : __builtin_ldexpf(1.0f, min(ezref - E, 127));
       const size_t slot = (size_t)s * p.BH + bh;
       uint16_t* Ts = p.T + slot * (size_t)(FT::NGB * DVP * 64);
       uint16_t* Zs = p.Z + slot * (size_t)(FT::NGB * 64);

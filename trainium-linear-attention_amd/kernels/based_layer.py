@@ -45,7 +45,7 @@ def _layer_fused(q, k, v, q_sw, k_sw, window, eps):
     qc, kc, vc, qs, ks = (_aligned(x) for x in (q, k, v, q_sw, k_sw))
     out = torch.empty(b, h, t, dv, dtype=q.dtype, device=q.device)
     L = _lib.lib()
-    ws_bytes = int(L.la_based_chunked_workspace_bytes(b, h, t, d, dv, 64))
+    ws_bytes = int(L.la_based_chunked_workspace_bytes_dt(b, h, t, d, dv, 64, _lib.LA_BF16))
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=q.device)
     rc = L.la_based_layer_fwd(_lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.ptr(qs), _lib.ptr(ks),
                               _lib.dtype_code(q.dtype), _lib.ptr(out), _lib.dtype_code(out.dtype), b, h, t, d, dv,
