@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define LA_ABI_VERSION 9
+#define LA_ABI_VERSION 10
 
 /* element types */
 #define LA_F32 0
@@ -114,8 +114,10 @@ int la_based_parallel_fwd_packed(const void* q, const void* k, const void* v, in
  * recurrence (128-token chunks, state export and import); other shapes and fp32 inputs run the
  * segment-state path (state prefixes of 512-token segments in the feature basis, then each query
  * against its segment's prefix plus the quadratic form inside the segment; fp32 arithmetic
- * throughout for fp32 inputs), which has no state export (LA_ERR_UNSUPPORTED_DIM with
- * state_out_or_null set).  Both are linear in N.
+ * throughout for fp32 inputs), which has no state export here (LA_ERR_UNSUPPORTED_DIM with
+ * state_out_or_null set): a caller continues such a sequence with la_based_chunked_fwd_num_den
+ * and the state's contraction with phi(q) (the Python layer does this with
+ * la_taylor_feature_map and fp32 GEMMs).  Both are linear in N.
  */
 size_t la_based_chunked_workspace_bytes(int B, int H, int N, int d, int dv, int chunk);
 
@@ -138,6 +140,19 @@ int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dty
                          float scale, float eps, int normalize,
                          void* workspace, size_t workspace_bytes, float* state_out_or_null,
                          void* hip_stream);
+
+/*
+ * The two parts of the normalised output, separately: num_out (B,H,N,dv) fp32 the numerator
+ * sum_{u<=t} p_tu v_u and den_out (B,H,N) fp32 the denominator sum_{u<=t} p_tu (no eps), for
+ * callers that add terms of their own before dividing (e.g. an earlier segment's state applied
+ * to these queries, out = (num + phi(q) S) / (den + phi(q) z + eps)).  Both must be 4-byte
+ * aligned.  Every shape of la_based_chunked_fwd, with its workspace.  No reference counterpart
+ * (the reference's chunked kernel returns the numerator only, kernels/nki_attention_chunked.py:56).
+ */
+int la_based_chunked_fwd_num_den(const void* q, const void* k, const void* v, int in_dtype,
+                                 float* num_out, float* den_out, int B, int H, int N, int d, int dv,
+                                 int chunk, float scale, void* workspace, size_t workspace_bytes,
+                                 void* hip_stream);
 
 /*
  * la_based_chunked_fwd continuing from an initial state: the sequence is the prev_tokens

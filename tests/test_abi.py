@@ -28,7 +28,8 @@ def test_header_declares_expected_entry_points():
         "la_abi_version", "la_status_string", "la_based_parallel_workspace_bytes", "la_based_parallel_fwd",
         "la_based_parallel_pack", "la_based_parallel_fwd_packed", "la_based_chunked_workspace_bytes",
         "la_based_chunked_workspace_bytes_dt", "la_based_chunked_chunk_used", "la_based_chunked_fwd",
-        "la_based_chunked_fwd_continue", "la_based_chunked_fwd_noalloc", "la_sliding_window_fwd",
+        "la_based_chunked_fwd_continue", "la_based_chunked_fwd_noalloc", "la_based_chunked_fwd_num_den",
+        "la_sliding_window_fwd",
         "la_sliding_window_fwd_add", "la_based_layer_fwd", "la_based_decode_step", "la_based_decode_workspace_bytes",
         "la_based_decode_step_ws", "la_identity_workspace_bytes", "la_identity_linear_fwd",
         "la_taylor_feature_map"])
@@ -42,7 +43,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_status_strings():
     lib = _lib()
-    assert lib.la_abi_version() == 9
+    assert lib.la_abi_version() == 10
     for code in range(-10, 1):
         s = lib.la_status_string(code).decode()
         assert s and s != "unknown status"
@@ -153,6 +154,32 @@ def test_chunked_continue_argument_errors():
     assert call(17, ctypes.c_void_p((1 << 20) + 2)) == -8         # not 4-byte aligned
     assert call(18, -1) == -4                                     # prev_tokens
     assert call(19, ctypes.c_void_p((1 << 20) + 4096)) == -9      # state_out overlaps state_in
+    assert call(8, 0) == 0                                        # N = 0
+
+
+def test_chunked_num_den_argument_errors():
+    lib = _lib()
+    f = lib.la_based_chunked_fwd_num_den
+    need = lib.la_based_chunked_workspace_bytes(1, 1, 8, 16, 64, 64)
+    D = ctypes.c_void_p(1 << 21)
+    ok = [P, P, P, 1, P, D, 1, 1, 8, 16, 64, 64, 0.25, P, need, None]
+
+    def call(i, x):
+        a = list(ok)
+        a[i] = x
+        return f(*a)
+
+    assert call(5, None) == -1                                    # den_out required
+    assert call(5, ctypes.c_void_p((1 << 21) + 2)) == -8          # den_out not 4-byte aligned
+    assert call(4, None) == -1                                    # num_out
+    assert call(12, 0.0) == -4                                    # scale
+    assert call(11, 0) == -2                                      # chunk
+    assert call(9, 80) == -5                                      # d > 64
+    need64 = lib.la_based_chunked_workspace_bytes_dt(1, 1, 2000, 64, 64, 64, 1)
+    assert need64 > 0
+    a = list(ok)
+    a[8], a[9], a[14] = 2000, 64, need64 - 1
+    assert f(*a) == -6                                            # workspace too small
     assert call(8, 0) == 0                                        # N = 0
 
 

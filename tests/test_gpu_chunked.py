@@ -173,8 +173,10 @@ def test_fp32_inputs_route_to_exact_path():
 
 
 def test_other_head_dims_use_the_parallel_kernel():
+    """d = 80 is outside both chunked paths: the parallel kernel computes it, and a state
+    (which would have 3321 features) is refused."""
     K = _kernels()
-    q, k, v = rand_qkv(1, 2, 150, 32, 16, seed=0, dtype=torch.bfloat16)
+    q, k, v = rand_qkv(1, 2, 150, 80, 16, seed=0, dtype=torch.bfloat16)
     y = K.chunked_based_attn(*to_dev(q, k, v))
     want, _, _ = ref.based_dense(q, k, v)
     assert err(y.float(), want) < 3e-2

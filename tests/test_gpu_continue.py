@@ -102,4 +102,7 @@ def test_continue_errors():
         K.based_chunked(q, k, v, state_in=torch.zeros(1, 1, 153, 64, device="cuda"))   # width
     q2, k2, v2 = to_dev(*rand_qkv(1, 1, 8, 32, 64, seed=0, dtype=torch.bfloat16))
     with pytest.raises(RuntimeError):
-        K.based_chunked(q2, k2, v2, state_in=torch.zeros(1, 1, 561, 65, device="cuda"))   # d = 32
+        K.based_chunked(q2, k2, v2, state_in=torch.zeros(1, 1, 153, 65, device="cuda"))   # d = 32 has 561 features
+    q3, k3, v3 = to_dev(*rand_qkv(1, 1, 8, 80, 64, seed=0, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError):
+        K.based_chunked(q3, k3, v3, state_in=torch.zeros(1, 1, 3321, 65, device="cuda"))  # d = 80: no chunked path

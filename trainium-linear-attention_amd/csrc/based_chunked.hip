@@ -1156,6 +1156,7 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
       // v_rcp_f32 (1 ulp) instead of an IEEE division, and a select, keep this branch-free
       const float sc = p.normalize ? un * __builtin_amdgcn_rcpf(den + p.eps) : un;
       const int row = row0 + 32 * W + r;
+      if (!LAYER && p.den_out != nullptr && h == 0 && row < N) p.den_out[(size_t)hrow + row] = den;
       if constexpr (LAYER) {
         // handed to the softmax wave of these queries, which adds its branch and stores
 #pragma unroll
@@ -1444,6 +1445,7 @@ int launch_based_chunked(const ChunkedArgs& a, hipStream_t stream) {
   ChunkParams p = chunk_params(a.q, a.k, a.v, a.out, a.workspace, a.BH, a.N, a.dv, a.scale);
   p.state_out = a.state_out;
   p.state_in = a.state_in;
+  p.den_out = a.den_out;
   p.prev_tokens = (float)a.prev_tokens;
   p.eps = a.eps;
   p.normalize = a.normalize ? 1 : 0;

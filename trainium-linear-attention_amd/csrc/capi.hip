@@ -156,7 +156,7 @@ int la_based_chunked_chunk_used(int chunk) {
 static int chunked_common(const void* q, const void* k, const void* v, int in_dtype, void* out, int out_dtype, int B,
                           int H, int N, int d, int dv, int chunk, float scale, float eps, int normalize,
                           void* workspace, size_t workspace_bytes, const float* state_in, long long prev_tokens,
-                          float* state_out_or_null, void* hip_stream) {
+                          float* state_out_or_null, void* hip_stream, float* den_out = nullptr) {
   int rc = check_common(q, k, v, out, in_dtype, out_dtype, B, H, N, d, dv);
   if (rc != LA_OK) return rc;
   if (!finite_f(scale) || !(scale > 0.f) || !finite_f(eps) || eps < 0.f) return LA_ERR_BAD_SCALAR;
@@ -175,11 +175,13 @@ static int chunked_common(const void* q, const void* k, const void* v, int in_dt
     const size_t bytes = (size_t)B * H * 153 * (size_t)(dv + 1) * 4;
     if (o0 != nullptr && i0 < o0 + bytes && o0 < i0 + bytes) return LA_ERR_OVERLAP;
   }
+  if (den_out != nullptr && (reinterpret_cast<uintptr_t>(den_out) & 3)) return LA_ERR_BAD_ALIGNMENT;
   la::ChunkedArgs a{};
   a.q = q;
   a.k = k;
   a.v = v;
   a.out = out;
+  a.den_out = den_out;
   a.state_out = state_out_or_null;
   a.state_in = state_in;
   a.prev_tokens = state_in != nullptr ? prev_tokens : 0;
@@ -242,6 +244,14 @@ int la_based_chunked_fwd(const void* q, const void* k, const void* v, int in_dty
                          void* workspace, size_t workspace_bytes, float* state_out_or_null, void* hip_stream) {
   return chunked_common(q, k, v, in_dtype, out, out_dtype, B, H, N, d, dv, chunk, scale, eps, normalize, workspace,
                         workspace_bytes, nullptr, 0, state_out_or_null, hip_stream);
+}
+
+int la_based_chunked_fwd_num_den(const void* q, const void* k, const void* v, int in_dtype, float* num_out,
+                                 float* den_out, int B, int H, int N, int d, int dv, int chunk, float scale,
+                                 void* workspace, size_t workspace_bytes, void* hip_stream) {
+  if (den_out == nullptr && (long long)B * H * N != 0) return LA_ERR_NULL_POINTER;
+  return chunked_common(q, k, v, in_dtype, num_out, LA_F32, B, H, N, d, dv, chunk, scale, 0.0f, 0, workspace,
+                        workspace_bytes, nullptr, 0, nullptr, hip_stream, den_out);
 }
 
 }  // extern "C"

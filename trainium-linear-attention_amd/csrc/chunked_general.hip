@@ -44,6 +44,7 @@ struct GParams {
   uint16_t* KV;     // converted chunks [BH][chunks before the last segment][GChunk rows][64]
   u32x2* CE;        // their exponents {Ec, Ez}
   float* Tot;       // per (part < nparts - 1, head, state work-group, thread): its part's sums
+  float* den_out;   // optional (BH, N): each row's denominator without eps
   int nparts, spp;  // the state sweep split into parts of spp segments
   int BH, N, d, dv, nseg, vec;
   float scale, eps;
@@ -699,6 +700,7 @@ __global__ __launch_bounds__(256, DVT == 4 ? 1 : 2) void gout_kernel(const GPara
     const float inv = p.normalize ? 1.0f / (dd + p.eps) : 1.0f;
     const int tok = t0 + 64 * w + 32 * nt + n;
     if (tok >= N) continue;
+    if (h == 0 && p.den_out != nullptr) p.den_out[(size_t)bh * N + tok] = dd;
     const size_t ob = ((size_t)bh * N + tok) * dv;
 #pragma unroll
     for (int mt = 0; mt < DVT; ++mt)
@@ -835,6 +837,7 @@ int launch_general_chunked(const ChunkedArgs& a, hipStream_t stream) {
   p.k = static_cast<const uint16_t*>(a.k);
   p.v = static_cast<const uint16_t*>(a.v);
   p.out = a.out;
+  p.den_out = a.den_out;
   p.BH = a.BH;
   p.N = a.N;
   p.d = a.d;

@@ -33,6 +33,7 @@ struct G32Params {
   float* T;      // [seg-1][BH][F][DVP]
   float* Z;      // [seg-1][BH][F]
   float* Tot;    // per (part < nparts - 1, head, state work-group, thread): its part's sums
+  float* den_out;   // optional (BH, N): each row's denominator without eps
   int nparts, spp;
   int BH, N, d, dv, nseg;
   float scale, eps;
@@ -372,6 +373,7 @@ __global__ __launch_bounds__(256, DVT == 4 ? 1 : 2) void g32_out_kernel(const G3
   // ---- out = num / (den + eps)
   den += __shfl_xor(den, 32);
   const float inv = p.normalize ? 1.0f / (den + p.eps) : 1.0f;
+  if (tok_ok && h == 0 && p.den_out != nullptr) p.den_out[(size_t)bh * N + tok] = den;
   if (tok_ok) {
     const size_t ob = ((size_t)bh * N + tok) * dv;
 #pragma unroll
@@ -471,6 +473,7 @@ int launch_general_chunked_f32(const ChunkedArgs& a, hipStream_t stream) {
   p.k = static_cast<const float*>(a.k);
   p.v = static_cast<const float*>(a.v);
   p.out = a.out;
+  p.den_out = a.den_out;
   p.BH = a.BH;
   p.N = a.N;
   p.d = a.d;

@@ -117,6 +117,7 @@ struct ChunkParams {
   float st_inv[4];                   // their inverses (initial state import)
   const float* state_in;             // optional initial state, reference basis (BH, 153, dv + 1)
   float prev_tokens;                 // tokens summarised by state_in (0 without one)
+  float* den_out;                    // optional (BH, N): each row's denominator without eps
   int normalize, out_f32, vec_out;
   // full layer (chunked_layer_kernel): the sliding-window softmax branch's q_sw, k_sw (BH, N, dsw)
   // bf16, its window and scale * log2(e)

@@ -43,6 +43,7 @@ struct ChunkedArgs {
   float* state_out;    // optional, (BH, F, dv + 1) fp32
   const float* state_in;   // optional initial state, same layout
   long long prev_tokens;   // tokens summarised by state_in
+  float* den_out;      // optional, (BH, N) fp32: each row's denominator without eps
   void* workspace;
   size_t workspace_bytes;
   int BH, N, d, dv, chunk;

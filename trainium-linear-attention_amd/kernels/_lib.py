@@ -45,6 +45,8 @@ _SIGNATURES = {
     "la_based_chunked_fwd": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
                                       _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int, _c_void,
                                       _c_size, _c_void, _c_void]),
+    "la_based_chunked_fwd_num_den": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_void, _c_int, _c_int,
+                                              _c_int, _c_int, _c_int, _c_int, _c_float, _c_void, _c_size, _c_void]),
     "la_based_chunked_fwd_noalloc": (_c_int, [_c_void, _c_void, _c_void, _c_int, _c_void, _c_int, _c_int, _c_int,
                                               _c_int, _c_int, _c_int, _c_int, _c_float, _c_float, _c_int, _c_void,
                                               _c_void]),
@@ -69,7 +71,7 @@ _SIGNATURES = {
     "la_taylor_feature_map": (_c_int, [_c_void, _c_int, _c_void, _c_int, ctypes.c_longlong, _c_int, _c_void]),
 }
 
-EXPECTED_ABI = 9
+EXPECTED_ABI = 10
 
 
 class BasedLAError(RuntimeError):

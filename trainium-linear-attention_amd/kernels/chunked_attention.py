@@ -77,6 +77,9 @@ def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, 
     ``state_in`` (same layout, e.g. an earlier call's state) continues a sequence: these tokens
     follow the ``prev_tokens`` tokens it summarises (default: its count entry z[0] of head 0,
     read back to the host), through ``la_based_chunked_fwd_continue``; it is not modified.
+    On the segment-state shapes (d != 16, dv > 64, fp32 inputs) both go through
+    ``la_based_chunked_fwd_num_den`` and fp32 GEMMs on phi (see _segment_state_with_state),
+    and the count of ``state_in`` is its own z[0] (``prev_tokens`` is not used).
     """
     _check_qkv(q, k, v)
     if int(chunk_size) < 1:
@@ -84,17 +87,23 @@ def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, 
     b, h, t, d = q.shape
     dv = v.shape[-1]
     cdt = _compute_dtype(q.dtype)
-    if not chunked_supported(d, dv, cdt):
-        if return_state or state_in is not None:
-            raise _lib.BasedLAError("state export and import need the chunked kernel (bf16, d = 16, dv <= 64)")
-        if not general_chunked_supported(d, dv, cdt):
-            from .pytorch_attention import based_parallel
-            return based_parallel(q, k, v, eps=eps, scale=scale, normalize=normalize, out_dtype=out_dtype)
+    with_state = return_state or state_in is not None
+    if not chunked_supported(d, dv, cdt) and not general_chunked_supported(d, dv, cdt):
+        if with_state:
+            raise _lib.BasedLAError(f"state export and import need d <= 64, dv <= 128 (got d={d}, dv={dv})")
+        from .pytorch_attention import based_parallel
+        return based_parallel(q, k, v, eps=eps, scale=scale, normalize=normalize, out_dtype=out_dtype)
     odt = q.dtype if out_dtype is None else out_dtype
     kdt = odt if odt in (torch.float32, torch.bfloat16) else torch.float32
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     qc, kc, vc = (_as_kernel_input(x, cdt) for x in (q, k, v))
+    if with_state and not chunked_supported(d, dv, cdt):
+        out, state = _segment_state_with_state(qc, kc, vc, cdt, kdt, int(chunk_size), float(scale), float(eps),
+                                               normalize, return_state, state_in)
+        if out.dtype != odt:
+            out = out.to(odt)
+        return (out, state) if return_state else out
     out = torch.empty(b, h, t, dv, dtype=kdt, device=q.device)
     L = _lib.lib()
     ws_bytes = int(L.la_based_chunked_workspace_bytes_dt(b, h, t, d, dv, int(chunk_size), _lib.dtype_code(cdt)))
@@ -123,6 +132,98 @@ def based_chunked(q, k, v, chunk_size=64, eps=1e-6, scale=None, normalize=True, 
     if out.dtype != odt:
         out = out.to(odt)
     return (out, state) if return_state else out
+
+
+def _phi_f32(x, a, L):
+    """phi(a x) in fp32 for rows x (n, t, d) by la_taylor_feature_map; a = 1 keeps x as it is."""
+    n, t, d = x.shape
+    xs = x if a == 1.0 else (x.float() * a)
+    out = torch.empty(n, t, feature_dim(d), dtype=torch.float32, device=x.device)
+    if n * t == 0:
+        return out
+    rc = L.la_taylor_feature_map(_lib.ptr(xs), _lib.dtype_code(xs.dtype), _lib.ptr(out), _lib.LA_F32, n * t, d,
+                                 _lib.stream_of(x))
+    _lib.check(rc, "la_taylor_feature_map")
+    return out
+
+
+# fp32 phi(Q) / phi(K) of at most this many bytes per pass over a group of heads
+_PHI_BYTES = 1 << 30
+
+
+def _segment_state_with_state(qc, kc, vc, cdt, kdt, chunk, scale, eps, normalize, return_state, state_in):
+    """State export and import for the segment-state shapes (d != 16, dv > 64 or fp32 inputs).
+
+    The kernels of la_based_chunked_fwd_num_den give every row's numerator and denominator over
+    these tokens from a zero state; the state enters as plain fp32 GEMMs in the reference
+    feature basis, with phi from la_taylor_feature_map at phi(a x), a = (scale^2 d)^(1/4), so
+    that phi(a q) . phi(a k) = 1 + s + s^2 / 2 for s = scale q.k (a = 1 at scale = 1/sqrt(d)):
+      import:  num += phi(a Q) S_in[:, :dv],  den += phi(a Q) S_in[:, dv]   (every query row)
+      export:  [S | z] = S_in + phi(a K)^T [V | 1]
+    The layout of the states is the recurrence path's ((b, h, F, dv + 1), fp32), so states pass
+    between the two paths and to based_decode_step (which evaluates phi at scale 1/sqrt(d)).  The
+    token count of state_in is its own z[0]; no separate count is needed.
+    """
+    b, h, t, d = qc.shape
+    dv = vc.shape[-1]
+    F = feature_dim(d)
+    dev = qc.device
+    L = _lib.lib()
+    rows = b * h
+    a = math.sqrt(scale * math.sqrt(d))
+    if abs(a - 1.0) < 1e-7:
+        a = 1.0
+    if state_in is not None:
+        _lib.require_gpu(qc, state_in)
+        if state_in.dtype != torch.float32 or tuple(state_in.shape) != (b, h, F, dv + 1):
+            raise _lib.BasedLAError(f"state_in must be fp32 {(b, h, F, dv + 1)}")
+        sin = state_in.contiguous().view(rows, F, dv + 1)
+    ws_bytes = int(L.la_based_chunked_workspace_bytes_dt(b, h, t, d, dv, chunk, _lib.dtype_code(cdt)))
+    if ws_bytes == (1 << 64) - 1:
+        raise _lib.BasedLAError(f"chunked kernel does not support d={d}, dv={dv}, chunk={chunk}")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    if state_in is None:
+        out = torch.empty(b, h, t, dv, dtype=kdt, device=dev)
+        rc = L.la_based_chunked_fwd(
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.dtype_code(cdt), _lib.ptr(out), _lib.dtype_code(kdt),
+            b, h, t, d, dv, chunk, scale, eps, 1 if normalize else 0, _lib.ptr(ws), ws_bytes, None,
+            _lib.stream_of(qc))
+        _lib.check(rc, "la_based_chunked_fwd")
+    else:
+        num = torch.empty(b, h, t, dv, dtype=torch.float32, device=dev)
+        den = torch.empty(b, h, t, dtype=torch.float32, device=dev)
+        rc = L.la_based_chunked_fwd_num_den(
+            _lib.ptr(qc), _lib.ptr(kc), _lib.ptr(vc), _lib.dtype_code(cdt), _lib.ptr(num), _lib.ptr(den),
+            b, h, t, d, dv, chunk, scale, _lib.ptr(ws), ws_bytes, _lib.stream_of(qc))
+        _lib.check(rc, "la_based_chunked_fwd_num_den")
+    state = torch.empty(b, h, F, dv + 1, dtype=torch.float32, device=dev) if return_state else None
+    per_head = max(1, t * F * 4)
+    group = max(1, min(rows, _PHI_BYTES // per_head))
+    qf, kf, vf = qc.view(rows, t, d), kc.view(rows, t, d), vc.view(rows, t, dv)
+    for r0 in range(0, rows, group):
+        r1 = min(rows, r0 + group)
+        if state_in is not None and t > 0:
+            ext = torch.bmm(_phi_f32(qf[r0:r1], a, L), sin[r0:r1])          # (n, t, dv + 1)
+            num.view(rows, t, dv)[r0:r1] += ext[..., :dv]
+            den.view(rows, t)[r0:r1] += ext[..., dv]
+            del ext
+        if return_state:
+            so = state.view(rows, F, dv + 1)[r0:r1]
+            if t > 0:
+                vx = torch.ones(r1 - r0, dv + 1, t, dtype=torch.float32, device=dev)
+                vx[:, :dv] = vf[r0:r1].transpose(1, 2)
+                so.copy_(torch.bmm(vx, _phi_f32(kf[r0:r1], a, L)).transpose(1, 2))   # [V | 1]^T phi(K)
+                if state_in is not None:
+                    so += sin[r0:r1]
+            elif state_in is not None:
+                so.copy_(sin[r0:r1])
+            else:
+                so.zero_()
+    if state_in is not None:
+        out = num / (den + eps).unsqueeze(-1) if normalize else num
+        if out.dtype != kdt:
+            out = out.to(kdt)
+    return out, state
 
 
 def based_decode_step(q, k, v, state, eps=1e-6, normalize=True):
