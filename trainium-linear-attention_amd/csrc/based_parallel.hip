@@ -828,7 +828,7 @@ size_t vrange_bytes(int BH) { return (size_t)BH * VR * 4; }
 bool parallel_packed_shape(int d, int dv, bool in_f32) { return !in_f32 && packed_shape(d, dv); }
 
 size_t parallel_workspace_bytes(int BH, int N, int d, int dv, bool in_f32) {
-  if (in_f32) return f32_split_workspace_bytes(BH, N, dv);   // partials of the key split, or 0
+  if (in_f32) return f32_split_workspace_bytes(BH, N, d, dv);   // partials of a key split, or 0
   if (!packed_shape(d, dv)) return vrange_bytes(BH);
   const size_t nb64 = ((size_t)N + BN - 1) / BN;
   const int DV = dv <= 32 ? 32 : 64;

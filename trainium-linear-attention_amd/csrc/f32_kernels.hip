@@ -36,8 +36,9 @@ struct F32Params {
   float* den;
   const float* addend;   // sliding: optional fp32 addend of the output, or null
   float* part;           // BASED key split: partial numerators [BH][nslot][BM][dv], then row sums
-                         // [BH][nslot][BM] (null: no split)
+                         // [BH][nslot][BM] (null: no split); or f32_x6_split_kernel's partials
   int BH, N, d, dv, nqb, window, nslot;
+  int x6parts;           // f32_x6_split_kernel: parts per query block slot (0: not used)
   int vec;               // d % 4 == 0, dv % 4 == 0 and q, k, v 16-byte aligned: float4 loads
   int out_vec;           // out 16-byte (fp32) / 8-byte (bf16) aligned: 4-column stores
   float inv_c, inv_c2, fscale, eps, scale_log2;
@@ -600,6 +601,207 @@ __global__ __launch_bounds__(512) void f32_x6_kernel(const F32Params p) {
   }
 }
 
+// fp32 BASED on small grids with the keys split over work-groups (d <= 16, dv <= 64, 16-byte
+// rows): the three-term bf16 products of f32_x6_kernel, but work-group (part, head, 32-query block
+// qb) takes only key tiles 8 TPW part .. 8 TPW part + 8 TPW - 1 up to the diagonal one, TPW tiles
+// per wave, so the longest serial chain is TPW tiles instead of ud / 8 + 1.  The operands go from
+// global memory (L2) straight into MFMA registers, without LDS tables: lane (key n, half h) loads
+// dims 8h .. 8h + 7 of its key for the score A operand, and element e of the V^T A operand of lane
+// (column n, half h) is V[key 16 m + 8 (e / 4) + 4 h + e % 4][32 mt + n] (the score accumulator's
+// row order), one coalesced 4-byte load per element.  The waves' numerators and row sums are added
+// through LDS in wave order; a query block with a single part normalises and stores, the others
+// write their partial numerators [query][DV] and row sums [query] to p.part for
+// f32_x6_combine_kernel.
+constexpr int X6_TPW = 2;   // key tiles per wave of f32_x6_split_kernel (1: 16.0, 2: 13.4, unsplit 14.6 us at B1 H4 N1024)
+template <int MT>
+__global__ __launch_bounds__(512, 2) void f32_x6_split_kernel(const F32Params p) {
+  constexpr int NW = 8, DV = 32 * MT, KT = 32, NSL = 4 * MT, TP = NW * X6_TPW;
+  __shared__ __attribute__((aligned(16))) float red[NW * NSL * 256 + NW * 64];
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, n = lane & 31;
+  const int N = p.N, d = p.d, dv = p.dv, nqb = p.nqb;
+  int g = blockIdx.x;
+  const int qb = nqb - 1 - g % nqb;   // the heaviest query blocks first
+  g /= nqb;
+  const int bh = g % p.BH, part = g / p.BH;
+  const int ud = min(qb, (N - 1) / KT);
+  const int nparts = ud / TP + 1;
+  if (part >= nparts) return;         // the whole work-group, before any barrier
+  const int q0 = KT * qb, query = q0 + n;
+  const size_t hrow = (size_t)bh * N;
+  const float* __restrict__ qg = p.q + hrow * d;
+  const float* __restrict__ kg = p.k + hrow * d;
+  const float* __restrict__ vg = p.v + hrow * dv;
+
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = splat16(0.f);
+  float rsum = 0.f;
+  u32x4 qf[3];
+  {
+    float xq[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 4) {
+      const int col = 8 * h + e;
+      f32x4 tq = {0.f, 0.f, 0.f, 0.f};
+      if (query < N && col < d) tq = *reinterpret_cast<const f32x4*>(qg + (size_t)query * d + col);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xq[e + i] = tq[i];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const Split3 a = split3_bf16x2(xq[2 * c], xq[2 * c + 1]);
+#pragma unroll
+      for (int r = 0; r < 3; ++r) qf[r][c] = a.t[r];
+    }
+  }
+#pragma unroll 1
+  for (int j = 0; j < X6_TPW; ++j) {
+    const int u = TP * part + w + NW * j;   // this wave's key tile
+    if (u > ud) break;
+    const int kb = KT * u;
+    // all loads of the tile first: the K row (two 16-byte loads), then the V elements
+    float xk[8], xv[MT][2][8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 4) {
+      const int col = 8 * h + e;
+      f32x4 tk = {0.f, 0.f, 0.f, 0.f};
+      if (kb + n < N && col < d) tk = *reinterpret_cast<const f32x4*>(kg + (size_t)(kb + n) * d + col);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xk[e + i] = tk[i];
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int key = kb + 16 * m + 8 * (e >> 2) + 4 * h + (e & 3), col = 32 * mt + n;
+          xv[mt][m][e] = (key < N && col < dv) ? vg[(size_t)key * dv + col] : 0.f;
+        }
+    u32x4 kf[3];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const Split3 b = split3_bf16x2(xk[2 * c], xk[2 * c + 1]);
+#pragma unroll
+      for (int r = 0; r < 3; ++r) kf[r][c] = b.t[r];
+    }
+    const f32x16 b = mfma_split3(kf, qf, splat16(p.inv_c));
+    // element i of lane (query n, half h) is key kb + c32_row(i, h)
+    const bool interior = kb + KT - 1 <= q0 && kb + KT <= N;
+    float pr[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int key = kb + c32_row(i, h);
+      const float pe = __builtin_fmaf(p.fscale, __builtin_fmaf(b[i], b[i], -p.inv_c2), 1.0f);
+      pr[i] = (interior || (key <= query && key < N)) ? pe : 0.f;
+      rsum += pr[i];
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      u32x4 pf[3];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const Split3 s3 = split3_bf16x2(pr[8 * m + 2 * c], pr[8 * m + 2 * c + 1]);
+#pragma unroll
+        for (int r = 0; r < 3; ++r) pf[r][c] = s3.t[r];
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        u32x4 vf[3];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const Split3 s3 = split3_bf16x2(xv[mt][m][2 * c], xv[mt][m][2 * c + 1]);
+#pragma unroll
+          for (int r = 0; r < 3; ++r) vf[r][c] = s3.t[r];
+        }
+        acc[mt] = mfma_split3(vf, pf, acc[mt]);
+      }
+    }
+  }
+
+  // wave-ordered sum, as in f32_x6_kernel: wave s < 4 MT adds slice s (four columns per lane)
+  const int nact = min(NW, ud + 1 - TP * part);
+  if (w < nact) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int gg = 0; gg < 4; ++gg)
+        *reinterpret_cast<f32x4*>(&red[((w * NSL + 4 * mt + gg) * 64 + lane) * 4]) =
+            (f32x4){acc[mt][4 * gg], acc[mt][4 * gg + 1], acc[mt][4 * gg + 2], acc[mt][4 * gg + 3]};
+    red[NW * NSL * 256 + w * 64 + lane] = rsum;
+  }
+  __syncthreads();
+  if (w >= NSL) return;
+  f32x4 y = {0.f, 0.f, 0.f, 0.f};
+  float rs = 0.f;
+  for (int ww = 0; ww < nact; ++ww) {
+    y += *reinterpret_cast<const f32x4*>(&red[((ww * NSL + w) * 64 + lane) * 4]);
+    rs += red[NW * NSL * 256 + ww * 64 + lane];
+  }
+  rs += __shfl_xor(rs, 32);
+  const int col = 32 * (w >> 2) + 8 * (w & 3) + 4 * h;
+  if (nparts > 1) {
+    const size_t slot = (size_t)(bh * nqb + qb) * p.x6parts + part;
+    *reinterpret_cast<f32x4*>(p.part + slot * (KT * DV) + n * DV + col) = y;
+    if (w == 0 && h == 0) p.part[(size_t)p.BH * nqb * p.x6parts * (KT * DV) + slot * KT + n] = rs;
+    return;
+  }
+  if (query >= N) return;
+  const float inv = p.normalize ? 1.0f / (rs + p.eps) : 1.0f;
+  if (p.den != nullptr && w == 0 && h == 0) p.den[hrow + query] = rs;
+  const size_t obase = (hrow + query) * (size_t)dv;
+  if (col < dv) {
+    if (p.out_f32)
+      *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + obase + col) = (f32x4){y[0] * inv, y[1] * inv, y[2] * inv, y[3] * inv};
+    else
+      *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + obase + col) =
+          (u32x2){pack_bf16x2(y[0] * inv, y[1] * inv), pack_bf16x2(y[2] * inv, y[3] * inv)};
+  }
+}
+
+// The parts of f32_x6_split_kernel's query blocks with more than one: work-group (query block,
+// head) adds the numerators and row sums of the parts in part order (all parts' loads issued
+// before the first add), normalises and stores.
+template <int MT>
+__global__ __launch_bounds__(256) void f32_x6_combine_kernel(const F32Params p) {
+  constexpr int KT = 32, DV = 32 * MT, PIECES = KT * DV / 4, NWP = 8;
+  const int nqb = p.nqb, qb = blockIdx.x, bh = blockIdx.y, N = p.N, dv = p.dv;
+  const int nparts = min(qb, (N - 1) / KT) / (8 * X6_TPW) + 1;
+  if (nparts == 1) return;
+  const size_t slot0 = (size_t)(bh * nqb + qb) * p.x6parts;
+  const float* dens = p.part + (size_t)p.BH * nqb * p.x6parts * (KT * DV);
+  const size_t hrow = (size_t)bh * N;
+  for (int pc = threadIdx.x; pc < PIECES; pc += 256) {
+    const int n = pc / (DV / 4), col = 4 * (pc % (DV / 4)), row = KT * qb + n;
+    if (row >= N || col >= dv) continue;
+    f32x4 x[NWP];
+    float t[NWP];
+#pragma unroll
+    for (int c = 0; c < NWP; ++c) {
+      const bool ok = c < nparts;
+      x[c] = ok ? *reinterpret_cast<const f32x4*>(p.part + (slot0 + c) * (KT * DV) + n * DV + col)
+                : (f32x4){0.f, 0.f, 0.f, 0.f};
+      t[c] = ok ? dens[(slot0 + c) * KT + n] : 0.f;
+    }
+    f32x4 y = x[0];
+    float den = t[0];
+#pragma unroll
+    for (int c = 1; c < NWP; ++c) {
+      y += x[c];
+      den += t[c];
+    }
+    if (p.den != nullptr && col == 0) p.den[hrow + row] = den;
+    const float inv = p.normalize ? 1.0f / (den + p.eps) : 1.0f;
+    const size_t o = (hrow + row) * (size_t)dv + col;
+    if (p.out_f32)
+      *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + o) = (f32x4){y[0] * inv, y[1] * inv, y[2] * inv, y[3] * inv};
+    else
+      *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(p.out) + o) =
+          (u32x2){pack_bf16x2(y[0] * inv, y[1] * inv), pack_bf16x2(y[2] * inv, y[3] * inv)};
+  }
+}
+
 // fp32 BASED on larger grids, with the three-term bf16 products of f32_x6_kernel: work-group
 // (head, 128 queries), wave w owns queries q0 + 32 w .. +31 and all DV columns.  The 32-key
 // tiles of K and V pass through LDS once per work-group as their three bf16 terms (K rows
@@ -784,6 +986,14 @@ int launch_f32(F32Params p, hipStream_t stream) {
       if ((long long)((p.N + 255) / 256) * p.BH >= 2LL * device_cu_count()) {
         p.nqb = (p.N + 255) / 256;
         hipLaunchKernelGGL((f32_x6_tiled_kernel<MT, 8>), dim3((unsigned)(p.nqb * p.BH)), dim3(512), 0, stream, p);
+      } else if (p.x6parts > 0) {
+        // query blocks of more than 8 key tiles: keys split over work-groups, then the combine
+        p.nqb = (p.N + 31) / 32;
+        hipLaunchKernelGGL(f32_x6_split_kernel<MT>, dim3((unsigned)(p.nqb * p.BH * p.x6parts)), dim3(512), 0, stream,
+                           p);
+        const int e = (int)hipGetLastError();
+        if (e != 0) return e;
+        hipLaunchKernelGGL(f32_x6_combine_kernel<MT>, dim3((unsigned)p.nqb, (unsigned)p.BH), dim3(256), 0, stream, p);
       } else {
         p.nqb = (p.N + 31) / 32;
         hipLaunchKernelGGL(f32_x6_kernel<MT>, dim3((unsigned)(p.nqb * p.BH)), dim3(512), 0, stream, p);
@@ -792,7 +1002,7 @@ int launch_f32(F32Params p, hipStream_t stream) {
     }
   }
   if constexpr (!SL) {
-    if (p.part != nullptr) {
+    if (p.part != nullptr && p.nslot > 0) {
       // key split over work-groups (the workspace was sized for it: f32_split_slots)
       hipLaunchKernelGGL((f32_attn_kernel<KS, MT, SL, 1, true>), dim3((unsigned)(p.BH * p.nslot)), dim3(256), 0,
                          stream, p);
@@ -840,10 +1050,23 @@ int f32_split_slots(int BH, int N) {
   return ns * BH <= 2048 ? (int)ns : 0;
 }
 
-size_t f32_split_workspace_bytes(int BH, int N, int dv) {
+// Parts per query block of f32_x6_split_kernel (8 key tiles of 32 each), or 0 when it is not
+// used: d > 16 or dv > 64, grids that f32_x6_tiled_kernel takes, and query blocks of at most 8
+// tiles (N <= 256) or more than 64 (N > 2048, where the partials would outweigh the gain).
+int f32_x6_split_parts(int BH, int N, int d, int dv) {
+  if (d > 16 || dv > 64 || BH < 1 || N < 1) return 0;
+  if ((long long)((N + 255) / 256) * BH >= 2LL * device_cu_count()) return 0;
+  const int pm = ((N + 31) / 32 + 8 * X6_TPW - 1) / (8 * X6_TPW);
+  return pm >= 2 && pm <= 8 ? pm : 0;
+}
+
+size_t f32_split_workspace_bytes(int BH, int N, int d, int dv) {
   const int ns = f32_split_slots(BH, N);
   const size_t cols = dv <= 32 ? 32 : (dv <= 64 ? 64 : 128);   // the kernel's 32 MT columns
-  return ns == 0 ? 0 : (size_t)BH * ns * 128 * (cols + 1) * sizeof(float);
+  const size_t old = ns == 0 ? 0 : (size_t)BH * ns * 128 * (cols + 1) * sizeof(float);
+  const int xp = f32_x6_split_parts(BH, N, d, dv);
+  const size_t x6 = xp == 0 ? 0 : (size_t)BH * ((N + 31) / 32) * xp * 32 * (cols + 1) * sizeof(float);
+  return old > x6 ? old : x6;
 }
 
 int launch_based_parallel_fp32(const ParallelArgs& a, hipStream_t stream) {
@@ -868,8 +1091,9 @@ int launch_based_parallel_fp32(const ParallelArgs& a, hipStream_t stream) {
           ((reinterpret_cast<uintptr_t>(a.k) & 15) == 0) && ((reinterpret_cast<uintptr_t>(a.v) & 15) == 0);
   p.out_vec = (reinterpret_cast<uintptr_t>(a.out) & (a.out_f32 ? 15 : 7)) == 0;
   p.nslot = f32_split_slots(a.BH, a.N);
-  if (p.nslot > 0) {
-    if (a.workspace == nullptr || a.workspace_bytes < f32_split_workspace_bytes(a.BH, a.N, a.dv))
+  p.x6parts = (p.vec && p.out_vec) ? f32_x6_split_parts(a.BH, a.N, a.d, a.dv) : 0;
+  if (p.nslot > 0 || p.x6parts > 0) {
+    if (a.workspace == nullptr || a.workspace_bytes < f32_split_workspace_bytes(a.BH, a.N, a.d, a.dv))
       return LA_ERR_WORKSPACE;
     p.part = static_cast<float*>(a.workspace);
   }

@@ -102,7 +102,8 @@ struct FeatureMapArgs {
 int launch_based_parallel(const ParallelArgs& a, hipStream_t stream);
 size_t parallel_workspace_bytes(int BH, int N, int d, int dv, bool in_f32);
 int f32_split_slots(int BH, int N);                         // fp32 key split: slots per head, or 0
-size_t f32_split_workspace_bytes(int BH, int N, int dv);    // its partials (0 without the split)
+int f32_x6_split_parts(int BH, int N, int d, int dv);       // fp32 three-term key split: parts, or 0
+size_t f32_split_workspace_bytes(int BH, int N, int d, int dv);   // partials of either split (or 0)
 bool parallel_packed_shape(int d, int dv, bool in_f32);   // shapes of the packed (pre-pass) kernel
 int launch_sliding_window(const SlidingArgs& a, hipStream_t stream);
 size_t chunked_workspace_bytes(int BH, int N, int d, int dv, int chunk);
