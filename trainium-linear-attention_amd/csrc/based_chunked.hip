@@ -75,7 +75,12 @@ struct OutLds {
   u32 xv[2][NWAVE_OUT];         // max |v| (bf16 bits) of the next chunk
   u32 xk[2][NWAVE_OUT];         // max |k| (bf16 bits) of the next chunk
   int eg;                       // exponent of G16
+  __attribute__((aligned(16))) u32 OS[NWAVE_OUT][32 * 32];   // per wave: its 32 output rows of a chunk (ost_off)
 };
+// Dword offset of 16-byte unit c (0..7) of row r in a wave's output staging rows: units are
+// XOR-swizzled by r & 7, so the accumulator-order writes (ds_write_b64 / b128, lanes r = 0..15)
+// and the row-order reads (ds_read_b128, eight lanes per row) hit distinct banks.
+__device__ __forceinline__ int ost_off(int r, int c) { return 32 * r + 4 * (c ^ (r & 7)); }
 // LDS image of the full-layer kernel: the chunk recurrence's tables with V^T in a ring of two
 // chunks (slot = absolute chunk index & 1: the softmax branch reads the previous chunk's keys),
 // the softmax branch's K_sw rows in a ring of two chunks, the chunk's linear-branch outputs
@@ -1166,20 +1171,42 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
             *reinterpret_cast<f32x4*>(&L.YL[(32 * W + r) * YLS + 32 * n + 8 * jj + 4 * h]) =
                 (f32x4){O[n][4 * jj] * sc, O[n][4 * jj + 1] * sc, O[n][4 * jj + 2] * sc, O[n][4 * jj + 3] * sc};
       } else if (VEC) {
+        // The wave's 32 x dv tile goes through its staging rows in LDS, so that every store
+        // instruction writes eight whole 128-byte row pieces (lane: row 8 i + l / 8, unit l % 8)
+        // instead of 16-byte pieces of 32 rows.  bf16: one pass of 64 columns; fp32: one pass per
+        // 32-column half.  Only this wave touches its rows (LDS operations of a wave complete in
+        // order).
         const __amdgpu_buffer_rsrc_t ro =
             make_rsrc(static_cast<char*>(p.out) + ((size_t)hrow + row0) * dv * esz, (u32)(N - row0) * (u32)dv * (u32)esz);
+        u32* os = L.OS[W];
+        const int rr = lane >> 3, cu = lane & 7;
+        if constexpr (OUT_F32) {
 #pragma unroll
-        for (int n = 0; n < 2; ++n) {
+          for (int n = 0; n < 2; ++n) {
 #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int col = 32 * n + 8 * jj + 4 * h;
-            const int voff = col < dv ? ((32 * W + r) * dv + col) * esz : kOffOutOfRange;
-            const float y0 = O[n][4 * jj] * sc, y1 = O[n][4 * jj + 1] * sc;
-            const float y2 = O[n][4 * jj + 2] * sc, y3 = O[n][4 * jj + 3] * sc;
-            if (OUT_F32)
-              buf_store_b128(__builtin_bit_cast(u32x4, (f32x4){y0, y1, y2, y3}), ro, voff);
-            else
-              buf_store_b64((u32x2){pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)}, ro, voff);
+            for (int jj = 0; jj < 4; ++jj)
+              *reinterpret_cast<f32x4*>(&os[ost_off(r, 2 * jj + h)]) =
+                  (f32x4){O[n][4 * jj] * sc, O[n][4 * jj + 1] * sc, O[n][4 * jj + 2] * sc, O[n][4 * jj + 3] * sc};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int row = 8 * i + rr, col = 32 * n + 4 * cu;
+              const u32x4 x = *reinterpret_cast<const u32x4*>(&os[ost_off(row, cu)]);
+              buf_store_b128(x, ro, col < dv ? ((32 * W + row) * dv + col) * 4 : kOffOutOfRange);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int n = 0; n < 2; ++n)
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+              *reinterpret_cast<u32x2*>(&os[ost_off(r, 4 * n + jj) + 2 * h]) =
+                  (u32x2){pack_bf16x2(O[n][4 * jj] * sc, O[n][4 * jj + 1] * sc),
+                          pack_bf16x2(O[n][4 * jj + 2] * sc, O[n][4 * jj + 3] * sc)};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int row = 8 * i + rr, col = 8 * cu;
+            const u32x4 x = *reinterpret_cast<const u32x4*>(&os[ost_off(row, cu)]);
+            buf_store_b128(x, ro, col < dv ? ((32 * W + row) * dv + col) * 2 : kOffOutOfRange);
           }
         }
       } else if (row < N) {
