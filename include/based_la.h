@@ -106,7 +106,8 @@ int la_based_parallel_fwd_packed(const void* q, const void* k, const void* v, in
  * chunked kernel returns); normalize = 1 divides by phi(q).z + eps like the parallel path.
  * state_out_or_null: optional fp32 output of the final state per head, (B,H,F,dv+1) with the
  * K-sum in the last column.  workspace: device scratch of at least
- * la_based_chunked_workspace_bytes(...) bytes (may be NULL when that is 0).
+ * la_based_chunked_workspace_bytes(...) bytes, 16-byte aligned (LA_ERR_BAD_ALIGNMENT otherwise;
+ * may be NULL when that size is 0).
  * chunk: the reference's chunk_size, any value >= 1 (LA_ERR_BAD_SHAPE below 1).  The recurrence
  * computes the same function for every chunk size (chunk-size invariance); it runs in chunks of
  * la_based_chunked_chunk_used(chunk) tokens.

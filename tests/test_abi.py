@@ -154,6 +154,7 @@ def test_chunked_continue_argument_errors():
     assert call(17, ctypes.c_void_p((1 << 20) + 2)) == -8         # not 4-byte aligned
     assert call(18, -1) == -4                                     # prev_tokens
     assert call(19, ctypes.c_void_p((1 << 20) + 4096)) == -9      # state_out overlaps state_in
+    assert call(15, ctypes.c_void_p((1 << 22) + 8)) == -8         # workspace not 16-byte aligned
     assert call(8, 0) == 0                                        # N = 0
 
 

@@ -165,6 +165,7 @@ static int chunked_common(const void* q, const void* k, const void* v, int in_dt
   const size_t need = la::chunked_scratch_bytes(B * H, N, d, dv, state_in != nullptr, in_dtype == LA_F32);
   if (need == (size_t)-1) return LA_ERR_UNSUPPORTED_DIM;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return LA_ERR_WORKSPACE;
+  if (need > 0 && (reinterpret_cast<uintptr_t>(workspace) & 15)) return LA_ERR_BAD_ALIGNMENT;   // 16-byte accesses
   if (state_out_or_null != nullptr && (reinterpret_cast<uintptr_t>(state_out_or_null) & 3)) return LA_ERR_BAD_ALIGNMENT;
   if (state_in != nullptr) {
     if (reinterpret_cast<uintptr_t>(state_in) & 3) return LA_ERR_BAD_ALIGNMENT;
