@@ -762,7 +762,7 @@ int launch_packed(const ParallelParams& pp, int stages, hipStream_t stream) {
                        dim3(256), 0,
                        stream, p.k, p.v, const_cast<uint16_t*>(p.vt), const_cast<float*>(p.stats), p.N, p.dv,
                        p.nb64);
-    hipLaunchKernelGGL(stats_scan_kernel, dim3((unsigned)p.BH, (unsigned)(stats_width(DV) / 16)), dim3(256), 0,
+    hipLaunchKernelGGL(stats_scan_kernel, dim3((unsigned)p.BH, (unsigned)(stats_width(DV) / 16 + 1)), dim3(256), 0,
                        stream, const_cast<float*>(p.stats), p.nb64, stats_width(DV), DV + kStatExpB,
                        const_cast<uint16_t*>(p.vt), VtBlockP<DV>::bytes / 2);
   }

@@ -186,8 +186,10 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
 // from nsum on (the exponent words) are left alone.  Work-group (bh, g) scans columns
 // 16 g .. 16 g + 15 of head bh in tiles of 256 blocks: 16 threads per column each sum a run of 16
 // blocks, a 16-term scan of the run totals gives each run's offset, and a carry links the tiles.
-// With vt set (the packed parallel pre-pass), the work-group of the last column group then
-// settles the head's V exponent (vt_head_exponent); other users scan every column (nsum = sw).
+// With vt set (the packed parallel pre-pass), one more work-group per head (the last column group
+// index) settles the head's V exponent (vt_head_exponent) beside the scans: it reads the block
+// exponent words and writes the head's, which no scan touches (columns from nsum on); other users
+// scan every column (nsum = sw).
 __device__ void vt_head_exponent(float* __restrict__ s, uint16_t* __restrict__ vt, int nb64, int sw, int vt_halves);
 
 __global__ __launch_bounds__(256) void stats_scan_kernel(float* __restrict__ stats, int nb64, int sw, int nsum,
@@ -195,6 +197,11 @@ __global__ __launch_bounds__(256) void stats_scan_kernel(float* __restrict__ sta
   constexpr int CW = 16, NT = 256 / CW, TB = 256, PER = TB / NT;
   __shared__ float tile[TB][CW + 1];
   __shared__ float tot[NT][CW];
+  if (vt != nullptr && (int)blockIdx.y == (int)gridDim.y - 1) {
+    vt_head_exponent(stats + (size_t)blockIdx.x * nb64 * sw + nsum, vt + (size_t)blockIdx.x * nb64 * vt_halves, nb64, sw,
+                     vt_halves);
+    return;
+  }
   const int tid = threadIdx.x, col = tid % CW, g = tid / CW;
   const bool summed = CW * (int)blockIdx.y + col < nsum;
   float* __restrict__ s = stats + (size_t)blockIdx.x * nb64 * sw + CW * blockIdx.y;
@@ -238,9 +245,6 @@ __global__ __launch_bounds__(256) void stats_scan_kernel(float* __restrict__ sta
     carry = all;
     __syncthreads();
   }
-  if (vt != nullptr && (int)blockIdx.y == (int)gridDim.y - 1)
-    vt_head_exponent(stats + (size_t)blockIdx.x * nb64 * sw + nsum, vt + (size_t)blockIdx.x * nb64 * vt_halves, nb64, sw,
-                     vt_halves);
 }
 
 // The head's V exponent E = max_b e_b over its blocks (e[b * sw] = e_b, written by the pack),
