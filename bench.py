@@ -14,7 +14,8 @@ headline workload (repeated to at least 10 s), on this host's cores.
 GPU time is measured with HIP events on the stream the kernels are launched on, around K
 back-to-back calls after W warm-up calls and at least --settle-ms (30) ms of back-to-back
 untimed calls, so that the card's clock has settled after the step from idle to load; HBM-bound configurations rotate through several
-input sets so that repeated calls do not run out of the 256 MB Infinity Cache.
+input sets so that repeated calls do not run out of the 256 MB Infinity Cache.  Each ``per_config``
+entry is the median of 5 such timed regions (``ms_reps``); the headline line times one.
 """
 
 from __future__ import annotations
@@ -23,6 +24,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 
@@ -189,11 +191,16 @@ class Call:
 # card's clock controller reacting to the load step) and settle at ~185 us after ~10 ms; with
 # idle gaps every call takes ~181 us.  Timing starts once the clock has settled.
 SETTLE_MS = 30.0
+# timed regions per benchmark configuration (`per_config` reports their median); the headline
+# line times exactly --steps calls once
+CONFIG_REPS = 5
 
 
-def time_calls(calls, steps, warmup, settle_ms=None):
+def time_calls(calls, steps, warmup, settle_ms=None, reps=1):
     """Mean ms per call over ``steps`` back-to-back launches (HIP events on the launch stream),
-    after at least ``warmup`` untimed calls and at least ``settle_ms`` of back-to-back work."""
+    after at least ``warmup`` untimed calls and at least ``settle_ms`` of back-to-back work.  With
+    ``reps`` > 1: that many timed regions of ``steps`` calls one after another, and the list of
+    their means."""
     import torch
 
     settle_ms = SETTLE_MS if settle_ms is None else settle_ms
@@ -206,14 +213,17 @@ def time_calls(calls, steps, warmup, settle_ms=None):
         if i % 8 == 0:
             torch.cuda.synchronize()   # host time then tracks the GPU's
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
-        calls[i % len(calls)]()
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    out = []
+    for _ in range(reps):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            calls[i % len(calls)]()
+        end.record()
+        torch.cuda.synchronize()
+        out.append(start.elapsed_time(end) / steps)
+    return out[0] if reps == 1 else out
 
 
 def chunk_run(chunk):
@@ -224,7 +234,9 @@ def chunk_run(chunk):
     return c
 
 
-def measure(cfg, steps, warmup, rotate, device, main_only=False):
+def measure(cfg, steps, warmup, rotate, device, main_only=False, reps=1):
+    """ms per call of one configuration; with reps > 1 the median of that many timed regions of
+    ``steps`` calls each (their means in ``ms_reps``)."""
     name, kind, B, H, N, d, dv, dt, seed, chunk, window, prescale = cfg
     esz = 2 if dt == "bf16" else 4
     crun = chunk_run(chunk) if kind == "chunked" else chunk
@@ -237,7 +249,8 @@ def measure(cfg, steps, warmup, rotate, device, main_only=False):
     for r in range(nsets):
         q, k, v = make_inputs(B, H, N, d, dv, dt, seed + 1000 * r, prescale, device)
         calls.append(Call(kind, q, k, v, chunk, window, main_only=main_only))
-    ms = time_calls(calls, steps, warmup)
+    ms_reps = time_calls(calls, steps, warmup, reps=reps) if reps > 1 else None
+    ms = statistics.median(ms_reps) if reps > 1 else time_calls(calls, steps, warmup)
     peak = PEAK_BF16_TFLOPS if dt == "bf16" else PEAK_FP32_TFLOPS
     t_mfma = flop / (peak * 1e12)
     t_hbm = nbytes / (PEAK_HBM_GBS * 1e9)
@@ -255,6 +268,8 @@ def measure(cfg, steps, warmup, rotate, device, main_only=False):
                   **({"window": window} if kind == "sliding" else {})},
         "input_sets": nsets,
     }
+    if ms_reps is not None:
+        res["ms_reps"] = [round(x, 5) for x in ms_reps]
     if kind == "chunked":
         res["tflops_f153"] = round(B * H * N * (4 * feature_dim(d) * dv + (chunk + 1) * (d + dv)) / sec / 1e12, 3)
     del calls
@@ -643,7 +658,7 @@ def main():
     if args.configs == "all":
         for cfg in CONFIGS:
             try:
-                per_config[cfg[0]] = measure(cfg, args.steps, args.warmup, args.rotate, device)
+                per_config[cfg[0]] = measure(cfg, args.steps, args.warmup, args.rotate, device, reps=CONFIG_REPS)
             except RuntimeError as e:
                 per_config[cfg[0]] = {"error": str(e)}
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_chunk_heads)
