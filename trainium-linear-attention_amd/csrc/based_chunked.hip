@@ -898,8 +898,8 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
   const uint16_t* kh = p.k + hrow * 16;
   const uint16_t* vh = p.v + hrow * dv;
   const int nchunks_total = (N + CH - 1) / CH;
-  const int c0 = seg * p.seg_chunks;
-  const int nch = min(p.seg_chunks, nchunks_total - c0);
+  const int c0 = seg * p.ostride * p.seg_chunks;
+  const int nch = min(p.ostride * p.seg_chunks, nchunks_total - c0);
   constexpr int esz = OUT_F32 ? 4 : 2;
 
   // k-side rows of the owned slots
@@ -935,7 +935,7 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
   if (seg > 0 || p.state_in != nullptr) {
     // prefix of the earlier segments (with the caller's initial state, when there is one); the
     // first segment's is slot P - 1, which holds the initial state alone
-    const size_t slot = (size_t)bh * p.P + (seg > 0 ? seg - 1 : p.P - 1);
+    const size_t slot = (size_t)bh * p.P + (seg > 0 ? seg * p.ostride - 1 : p.P - 1);
     U = seg > 0 ? p.wsEP[slot] : p.wsE[slot];
     const uint16_t* ws = p.wsS + slot * (64 * NF);
 #pragma unroll
@@ -1289,7 +1289,7 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
 
   // ---- final state of the head (last segment) in the reference feature basis, fp32:
   // state_out[f][0..dv) = sum_u phi_f(k_u) v_u, state_out[f][dv] = sum_u phi_f(k_u)
-  if (!LAYER && p.state_out != nullptr && seg == p.P - 1) {
+  if (!LAYER && p.state_out != nullptr && (seg + 1) * p.ostride >= p.P) {
     float* so = p.state_out + (size_t)bh * 153 * (dv + 1);
     // the Gram matrix in fp32 for the k-sums: G32[i][j], 32 x 33 floats over the S^T table
     float* G32 = reinterpret_cast<float*>(L.ST);
@@ -1351,7 +1351,7 @@ __global__ __launch_bounds__(64 * 2 * NWAVE_OUT, 1) void chunked_layer_kernel(co
   __shared__ __attribute__((aligned(16))) LayerLds<DSW> L;
   using LT = LayerLds<DSW>;
   int bh, seg;
-  map_segment(blockIdx.x, p.BH, p.P, bh, seg);
+  map_segment(blockIdx.x, p.BH, (p.P + p.ostride - 1) / p.ostride, bh, seg);
   switch (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) {
     case 0: output_wave<0, true, OUT_F32, LT, DSW>(L, p, bh, seg); break;
     case 1: output_wave<1, true, OUT_F32, LT, DSW>(L, p, bh, seg); break;
@@ -1416,6 +1416,7 @@ ChunkParams chunk_params(const void* q, const void* k, const void* v, void* out,
   segment_split(BH, N, P, seg_chunks);
   p.P = P;
   p.seg_chunks = seg_chunks;
+  p.ostride = 1;
   const size_t nslot = (size_t)BH * P;
   char* ws = static_cast<char*>(workspace);
   p.wsS = reinterpret_cast<uint16_t*>(ws);
@@ -1512,7 +1513,11 @@ int launch_based_layer(const LayerArgs& a, hipStream_t stream) {
   p.sw_log2 = (float)((double)a.scale_sw * 1.4426950408889634);
   const int e = launch_increments(p, true, stream);
   if (e != 0) return e;
-  const dim3 grid((unsigned)(a.BH * p.P)), block(64 * 2 * NWAVE_OUT);
+  // one 8-wave work-group per CU: when the (head, segment) work-groups would need more than one
+  // round of the CUs, each takes two consecutive segments from the first one's prefix (one round,
+  // one fixed phase per work-group instead of two)
+  if (p.P >= 2 && (long long)a.BH * p.P > device_cu_count()) p.ostride = 2;
+  const dim3 grid((unsigned)(a.BH * ((p.P + p.ostride - 1) / p.ostride))), block(64 * 2 * NWAVE_OUT);
 #define LA_LAYER(F32, D) hipLaunchKernelGGL((chunked_layer_kernel<F32, D>), grid, block, 0, stream, p)
   if (a.dsw == 16) {
     if (a.out_f32) LA_LAYER(true, 16); else LA_LAYER(false, 16);

@@ -111,6 +111,8 @@ struct ChunkParams {
   int* wsE;         // [BH][P] exponent of each increment (slot P - 1: the imported state)
   int* wsEP;        // [BH][P] exponent of each prefix
   int BH, N, dv, P, seg_chunks;
+  int ostride;      // increment segments per output segment (the output pass's work-group covers
+                    // ostride consecutive segments, starting from the prefix of the first)
   float qs, ks;                      // q~ = qs q (= sqrt(scale) q); K^T table rows ks k = q~-scale k / 2
   float eps;
   float st_fac[4];                   // k side of 2p -> reference feature factors (state export)
