@@ -117,7 +117,8 @@ def _layer_inputs(B, H, N, dv, d_sw, seed, vscale=1.0):
     (2, 3, 1100, 24, 32, 17),    # dv < 64 (columns past dv), d_sw 32, ragged last chunk
     (1, 1, 700, 8, 16, 1),       # window 1: the diagonal only
     (1, 2, 257, 64, 64, 33),     # window 33: the first key tile is outside every window
-    (2, 16, 2048, 64, 64, 64),   # 32 heads, 16 segments each
+    (2, 16, 2048, 64, 64, 64),   # 32 heads, 16 segments each: two per layer work-group
+    (2, 16, 1900, 64, 64, 64),   # 15 segments: two per layer work-group, the last one alone
     (1, 1, 9000, 64, 64, 50),    # several chunks per segment
 ])
 def test_fused_layer_matches_oracle(B, H, N, dv, d_sw, W):
@@ -154,6 +155,25 @@ def test_fused_layer_v_range(case):
     errs = [ref.rel_err(y[0, hh].cpu(), want[0, hh]) for hh in range(H)]
     print(f"{case}: per-head err " + " ".join(f"{x:.2e}" for x in errs))
     assert max(errs) < 2e-2
+
+
+def test_fused_layer_v_steps_two_segments_per_work_group():
+    """32 heads of 16 one-chunk segments, so that each layer work-group runs two segments from the
+    first one's prefix: V 1e-4 for the first 700 tokens and 300 from token 1450 on (inside the
+    second segment of a work-group), against the fp64 oracle on four heads."""
+    B, H, N, dv, d_sw, W = 2, 16, 2048, 64, 64, 64
+    q, k, v, q_sw, k_sw = _layer_inputs(B, H, N, dv, d_sw, seed=23)
+    t = torch.ones(1, 1, N, 1)
+    t[:, :, :700] = 1e-4
+    t[:, :, 1450:] = 300.0
+    v = (v.float() * t).bfloat16()
+    y = _fused(*to_dev(q, k, v, q_sw, k_sw), W, torch.float32)
+    for b, hh in ((0, 0), (0, 7), (1, 8), (1, 15)):
+        sl = (slice(b, b + 1), slice(hh, hh + 1))
+        want = ref.based_layer_dense(q[sl], k[sl], v[sl], window_size=W, q_sw=q_sw[sl], k_sw=k_sw[sl])
+        e = ref.rel_err(y[sl].cpu(), want)
+        print(f"v steps, head ({b}, {hh}): err={e:.3e}")
+        assert e < 2e-2
 
 
 def test_fused_layer_b2h16n8192():
