@@ -404,6 +404,9 @@ def test_feature_map_argument_errors():
     assert f(P, 5, P, 0, 4, 16, None) == -3
     assert f(P, 0, P, 0, 4, 200, None) == -5
     assert f(P, 0, P, 0, 0, 16, None) == 0
+    # rows * F beyond 2^40 elements (and far beyond, where the product would overflow int64)
+    assert f(P, 0, P, 0, (1 << 40) // 153 + 1, 16, None) == -2
+    assert f(P, 0, P, 0, (1 << 62), 16, None) == -2
 
 
 def test_python_wrappers_refuse_cpu_tensors():

@@ -469,7 +469,7 @@ int la_taylor_feature_map(const void* x, int in_dtype, void* out, int out_dtype,
       (reinterpret_cast<uintptr_t>(out) & (out_dtype == LA_F32 ? 3 : 1)))
     return LA_ERR_BAD_ALIGNMENT;
   const long long F = 1 + (long long)d + (long long)d * (d + 1) / 2;
-  if (rows * F > (1LL << 40)) return LA_ERR_BAD_SHAPE;
+  if (rows > (1LL << 40) / F) return LA_ERR_BAD_SHAPE;   // rows * F elements, without overflow
   la::FeatureMapArgs a{};
   a.x = x;
   a.out = out;
