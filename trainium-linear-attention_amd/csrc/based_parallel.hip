@@ -401,7 +401,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
     // the head's V exponent from the VR partial maxima of vrange_kernel
     const u32 m = wave_max_u32(lane < VR ? p.vmax[(size_t)bh * VR + lane] : 0u);
     const int E = vexp_step(m << 16);
-    st.vscale = __builtin_ldexpf(1.0f, -E);
+    st.vexp = -E;
     vexp_f = __builtin_ldexpf(1.0f, E);
     st.load(kg, vg, 0, N, d, dv, tid);
     st.store(Ks[0], VTs[0], tid);

@@ -118,8 +118,8 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
       if (lane == 0) vmx[w] = m;
     }
     __syncthreads();   // image zeroed / the previous block's readers done / wave maxima written
+    // fp16(v 2^-eb) by ldexp on each value: exact, and finite for an all-zero block (eb = -128)
     const int eb = vexp_step(max(max(vmx[0], vmx[1]), max(vmx[2], vmx[3])) << 16);
-    const float vs = __builtin_ldexpf(1.0f, -eb);
     float part[8];
     if (tid < NT) {
 #pragma unroll
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
         const float f0 = (e & 1) ? bf16_hi_to_f32(a0) : bf16_lo_to_f32(a0);
         const float f1 = (e & 1) ? bf16_hi_to_f32(a1) : bf16_lo_to_f32(a1);
         part[e] = f0 + f1;
-        img[(col + e) * (ROW / 2) + kp] = pack_f16x2(f0 * vs, f1 * vs);
+        img[(col + e) * (ROW / 2) + kp] = pack_f16x2(__builtin_ldexpf(f0, -eb), __builtin_ldexpf(f1, -eb));
       }
     } else {
 #pragma unroll

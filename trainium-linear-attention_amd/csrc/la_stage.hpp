@@ -11,9 +11,10 @@ constexpr int BN = 64;        // keys per LDS block
 constexpr int VROW = BN + 4;  // V^T row stride (bf16): 34 dwords -> conflict-free 8-byte reads
 
 // Global -> register -> LDS staging of one 64-key block of K (row-major) and V (transposed).
-// F16V converts V from bf16 to fp16(v * vscale) on the way, vscale a power of two chosen by the
-// caller from max |v| so that the values land in fp16's normal range, so the P.V product can run
-// as an fp16 MFMA.
+// F16V converts V from bf16 to fp16(v 2^vexp) on the way, vexp chosen by the caller from max |v|
+// so that the values land in fp16's normal range, so the P.V product can run as an fp16 MFMA.
+// The power of two is applied by ldexp on each value, which is exact and stays finite for every
+// vexp (a factor 2^vexp would overflow for an all-zero V, whose vexp is 128 and up).
 template <int KS, int MT, bool VEC, bool F16V = false>
 struct BlockStager {
   static constexpr int DK = 16 * KS, DV = 32 * MT, KROW = DK + 8;
@@ -23,7 +24,7 @@ struct BlockStager {
   static constexpr int VPT = (VGROUPS + 255) / 256;
   u32x4 kr[KPT];
   u32x2 vr[VPT][4];
-  float vscale = 1.0f;   // F16V: V is stored as fp16(v * vscale), vscale a power of two
+  int vexp = 0;   // F16V: V is stored as fp16(v 2^vexp)
 
   __device__ __forceinline__ void load(const uint16_t* __restrict__ kg, const uint16_t* __restrict__ vg,
                                        int row0, int N, int d, int dv, int tid) {
@@ -91,15 +92,15 @@ struct BlockStager {
         const u32 b0 = vr[r][0][1], b1 = vr[r][1][1], b2 = vr[r][2][1], b3 = vr[r][3][1];
         u32x2 c0, c1, c2, c3;
         if (F16V) {
-          const float s = vscale;
-          c0 = (u32x2){pack_f16x2(bf16_lo_to_f32(a0) * s, bf16_lo_to_f32(a1) * s),
-                       pack_f16x2(bf16_lo_to_f32(a2) * s, bf16_lo_to_f32(a3) * s)};
-          c1 = (u32x2){pack_f16x2(bf16_hi_to_f32(a0) * s, bf16_hi_to_f32(a1) * s),
-                       pack_f16x2(bf16_hi_to_f32(a2) * s, bf16_hi_to_f32(a3) * s)};
-          c2 = (u32x2){pack_f16x2(bf16_lo_to_f32(b0) * s, bf16_lo_to_f32(b1) * s),
-                       pack_f16x2(bf16_lo_to_f32(b2) * s, bf16_lo_to_f32(b3) * s)};
-          c3 = (u32x2){pack_f16x2(bf16_hi_to_f32(b0) * s, bf16_hi_to_f32(b1) * s),
-                       pack_f16x2(bf16_hi_to_f32(b2) * s, bf16_hi_to_f32(b3) * s)};
+          const int s = vexp;
+          c0 = (u32x2){pack_f16x2(__builtin_ldexpf(bf16_lo_to_f32(a0), s), __builtin_ldexpf(bf16_lo_to_f32(a1), s)),
+                       pack_f16x2(__builtin_ldexpf(bf16_lo_to_f32(a2), s), __builtin_ldexpf(bf16_lo_to_f32(a3), s))};
+          c1 = (u32x2){pack_f16x2(__builtin_ldexpf(bf16_hi_to_f32(a0), s), __builtin_ldexpf(bf16_hi_to_f32(a1), s)),
+                       pack_f16x2(__builtin_ldexpf(bf16_hi_to_f32(a2), s), __builtin_ldexpf(bf16_hi_to_f32(a3), s))};
+          c2 = (u32x2){pack_f16x2(__builtin_ldexpf(bf16_lo_to_f32(b0), s), __builtin_ldexpf(bf16_lo_to_f32(b1), s)),
+                       pack_f16x2(__builtin_ldexpf(bf16_lo_to_f32(b2), s), __builtin_ldexpf(bf16_lo_to_f32(b3), s))};
+          c3 = (u32x2){pack_f16x2(__builtin_ldexpf(bf16_hi_to_f32(b0), s), __builtin_ldexpf(bf16_hi_to_f32(b1), s)),
+                       pack_f16x2(__builtin_ldexpf(bf16_hi_to_f32(b2), s), __builtin_ldexpf(bf16_hi_to_f32(b3), s))};
         } else {
           c0 = (u32x2){(a0 & 0xffffu) | (a1 << 16), (a2 & 0xffffu) | (a3 << 16)};
           c1 = (u32x2){(a0 >> 16) | (a1 & 0xffff0000u), (a2 >> 16) | (a3 & 0xffff0000u)};
