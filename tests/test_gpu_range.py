@@ -223,3 +223,20 @@ def test_general_zero_key_dims_large_v():
     errs = head_errs(y, want)
     print(f"general d64 zero key dims, v x 1e10: errs " + " ".join(f"{x:.2e}" for x in errs))
     assert torch.isfinite(y).all() and max(errs) < TOL
+
+
+@pytest.mark.parametrize("path,d,kscale", [("parallel", 16, 1e4), ("parallel", 32, 1e4), ("chunked", 16, 100.0),
+                                           ("chunked", 64, 30.0)])
+def test_unbalanced_q_k(path, d, kscale):
+    """q divided and k multiplied by the same factor (the scores are unchanged): the parallel
+    kernels at 1e4; the d = 16 chunk recurrence, whose features are fp16 products of
+    sqrt(scale) q and sqrt(scale) k, at 100 (max |k| about 450 here, inside its limit of 1024);
+    the bf16 segment-state path, whose q-side features are fp16 in units of max |[scale q, 1]|,
+    at 30 (the stated range of both)."""
+    q, k, v = rand_qkv(1, 2, 700, d, 64, seed=3, dtype=torch.float32)
+    q, k, v = (q / kscale).bfloat16(), (k * kscale).bfloat16(), v.bfloat16()
+    want, _, _ = ref.based_dense(q, k, v)
+    y = _run(path, q, k, v)
+    e = max(head_errs(y, want))
+    print(f"{path} d={d} q / {kscale:g}, k x {kscale:g}: err={e:.3e}")
+    assert torch.isfinite(y).all() and e < TOL

@@ -135,3 +135,24 @@ def test_zero_v_identity():
     e = max(head_errs(y, want))
     print(f"identity with zero V regions: err={e:.3e}")
     assert torch.isfinite(y).all() and e < 1e-3
+
+
+@pytest.mark.parametrize("which", ["q", "k"])
+@pytest.mark.parametrize("path,d,dv,dtype,B,H,N", CASES)
+def test_zero_q_or_k(path, d, dv, dtype, B, H, N, which):
+    """q or k zero everywhere (every score 0, p = 1: each output row is the running mean of v)."""
+    q, k, v = rand_qkv(B, H, N, d, dv, seed=N + 3 * d, dtype=torch.float32, scale_qk=0.5)
+    if which == "q":
+        q = torch.zeros_like(q)
+    else:
+        k = torch.zeros_like(k)
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    y = _run(path, q, k, v).cpu()
+    assert torch.isfinite(y).all(), f"{path} d={d} dv={dv} {dtype} zero {which}: non-finite outputs"
+    b, h = B - 1, H - 1
+    sl = (slice(b, b + 1), slice(h, h + 1))
+    want, _, _ = ref.based_dense(q[sl], k[sl], v[sl])
+    e = max(head_errs(y[sl], want))
+    tol = TOL_F32 if dtype == torch.float32 else TOL
+    print(f"{path} d={d} dv={dv} {dtype} zero {which}: err={e:.3e}")
+    assert e < tol
