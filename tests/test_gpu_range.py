@@ -240,3 +240,34 @@ def test_unbalanced_q_k(path, d, kscale):
     e = max(head_errs(y, want))
     print(f"{path} d={d} q / {kscale:g}, k x {kscale:g}: err={e:.3e}")
     assert torch.isfinite(y).all() and e < TOL
+
+
+@pytest.mark.parametrize("vscale", [1e-20, 1e-36, 1e30])
+@pytest.mark.parametrize("path,d,B,H,N", [("parallel", 16, 1, 2, 1100), ("parallel", 32, 1, 2, 1100),
+                                          ("chunked", 16, 1, 2, 3000), ("chunked", 16, 2, 16, 2600),
+                                          ("chunked", 64, 1, 2, 1500)])
+def test_v_extreme_scales(vscale, path, d, B, H, N):
+    """V at 1e-20, 1e-36 (near bf16's smallest normal) and 1e30: the fp16 copies of V and of the
+    chunked states carry power-of-two exponents (the d = 16 recurrence's unit no lower than
+    2^-126; the segment-state path divides V by the head's 2^floor(log2 max|v|) before its fp16
+    prefixes, which sit beside the k-sums), so every path holds the bf16 bar."""
+    q, k, v = _scaled(B, H, N, d, 64, seed=19, vscale=vscale)
+    sl = (slice(0, 1), slice(0, 1))
+    want, _, _ = ref.based_dense(q[sl], k[sl], v[sl])
+    y = _run(path, q, k, v)
+    e = max(head_errs(y[sl], want))
+    print(f"{path} d={d} B{B} H{H} N{N} v x {vscale:g}: err={e:.3e}")
+    assert torch.isfinite(y).all() and e < TOL
+
+
+def test_general_v_tiny_prefix():
+    """Segment-state path (d = 64): the first 600 tokens' V 1e-20 times the rest, so the first
+    segment's prefix is 1e-20 below the later ones (the head exponent comes from the largest)."""
+    q, k, v = _scaled(1, 2, 1500, 64, 64, seed=20)
+    t = torch.ones(1, 2, 1500, 1)
+    t[:, :, :600] = 1e-20
+    v = (v.float() * t).bfloat16()
+    want, _, _ = ref.based_dense(q, k, v)
+    errs = head_errs(_run("chunked", q, k, v), want)
+    print("general d64 tiny-V prefix errs " + " ".join(f"{x:.2e}" for x in errs))
+    assert max(errs) < TOL

@@ -220,16 +220,14 @@ __device__ __forceinline__ void stage_convert_v(const StageRegs& s, StageConv& o
   }
 }
 
-// fp16(v 2^e) by ldexp on each value: exact, and finite for every e (the unit of a work-group
-// that has seen only zero V is far below -127, where a factor 2^-U would be infinite).
-__device__ __forceinline__ void stage_convert_v_scaled(const StageRegs& s, StageConv& o, int e) {
+__device__ __forceinline__ void stage_convert_v_scaled(const StageRegs& s, StageConv& o, float vs) {
 #pragma unroll
   for (int pp = 0; pp < 2; ++pp) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const u32 a = s.v[pp][0][w], b = s.v[pp][1][w];
-      o.vt[pp][2 * w] = pack_f16x2(__builtin_ldexpf(bf16_lo_to_f32(a), e), __builtin_ldexpf(bf16_lo_to_f32(b), e));
-      o.vt[pp][2 * w + 1] = pack_f16x2(__builtin_ldexpf(bf16_hi_to_f32(a), e), __builtin_ldexpf(bf16_hi_to_f32(b), e));
+      o.vt[pp][2 * w] = pack_f16x2(bf16_lo_to_f32(a) * vs, bf16_lo_to_f32(b) * vs);
+      o.vt[pp][2 * w + 1] = pack_f16x2(bf16_hi_to_f32(a) * vs, bf16_hi_to_f32(b) * vs);
     }
   }
 }
@@ -280,16 +278,14 @@ __device__ __forceinline__ int next_unit(int U, int eS, int eV) {
   return n;
 }
 
-// S 2^e by ldexp on each value (exact, finite for every e: a zero state stays zero when the unit
-// rises from one far below -127).
 template <int NB>
-__device__ __forceinline__ void acc_scale(f32x16 (&S)[NB][2], int e) {
+__device__ __forceinline__ void acc_scale(f32x16 (&S)[NB][2], float f) {
 #pragma unroll
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int n = 0; n < 2; ++n)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) S[b][n][i] = __builtin_ldexpf(S[b][n][i], e);
+      for (int i = 0; i < 16; ++i) S[b][n][i] *= f;
 }
 
 // Keeps the conversion above this point (the compiler would otherwise sink it next to the LDS
@@ -436,7 +432,7 @@ __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_k
   Ux = first_unit(read_vexp(0, sub ^ 1));
   if (Uo != 0 || Ux != 0) {   // V outside [2^-6, 2^13): convert the first chunk again, scaled
     if (Uo != 0 && stager) {
-      stage_convert_v_scaled(sa, cv, -Uo);
+      stage_convert_v_scaled(sa, cv, __builtin_ldexpf(1.0f, -Uo));
       stage_write_v(cv, L.buf[0].VT, lane, w);
     }
     lds_barrier();
@@ -464,11 +460,11 @@ __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_k
     const int Uon = next_unit(Uo, kNoExp, read_vexp((c + 1) & 1, sub));
     const int Uxn = next_unit(Ux, kNoExp, read_vexp((c + 1) & 1, sub ^ 1));
     if (c + 1 < nch && (Uon != Uo || Uxn != Ux || Uon != 0 || Uxn != 0)) {
-      if (Uon != Uo) acc_scale<1>(S, Uo - Uon);
+      if (Uon != Uo) acc_scale<1>(S, __builtin_ldexpf(1.0f, Uo - Uon));
       if (Uon != 0 && more) {
         StageRegs again;
         stage_load<VEC_V, false>(again, p, nullptr, kh, vh, (c0 + c + 1) * CH, lane, w);
-        stage_convert_v_scaled(again, cv, -Uon);
+        stage_convert_v_scaled(again, cv, __builtin_ldexpf(1.0f, -Uon));
         stage_write_v(cv, L.buf[(c + 1) & 1].VT, lane, w);
       }
       Uo = Uon;
@@ -498,17 +494,18 @@ __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_k
   for (int i = 0; i < NWAVE_SEG; ++i) msub = max(msub, smx[sub][i]);
   msub = (u32)__builtin_amdgcn_readfirstlane((int)msub);
   const int eS = exp_of_f32bits(msub);
-  const int EI = eS == kNoExp ? kNoExp : Uo + eS - 13;
-  // S 2^(13 - eS) by ldexp on each value (exact; finite where a factor would overflow)
-  const int es = eS == kNoExp ? 0 : 13 - eS;
+  // S 2^es in fp16, es = 13 - eS, clamped so that the factor stays finite (the stored exponent
+  // follows the clamp; a state more than 2^114 below 1 in units of 2^Uo has lost nothing of use)
+  const int es = eS == kNoExp ? 0 : min(13 - eS, 127);
+  const int EI = eS == kNoExp ? kNoExp : Uo - es;
+  const float f = eS == kNoExp ? 0.f : __builtin_ldexpf(1.0f, es);
 #pragma unroll
   for (int n = 0; n < (active ? 2 : 0); ++n) {
 #pragma unroll
     for (int J = 0; J < 2; ++J) {
       const f32x16& a = S[0][n];
-      auto sc = [&](int i) { return __builtin_ldexpf(a[8 * J + i], es); };
-      const u32x4 pk = {pack_f16x2(sc(0), sc(1)), pack_f16x2(sc(2), sc(3)), pack_f16x2(sc(4), sc(5)),
-                        pack_f16x2(sc(6), sc(7))};
+      const u32x4 pk = {pack_f16x2(a[8 * J + 0] * f, a[8 * J + 1] * f), pack_f16x2(a[8 * J + 2] * f, a[8 * J + 3] * f),
+                        pack_f16x2(a[8 * J + 4] * f, a[8 * J + 5] * f), pack_f16x2(a[8 * J + 6] * f, a[8 * J + 7] * f)};
       *reinterpret_cast<u32x4*>(&ws[(32 * n + r) * NF + 32 * w + 16 * J + 8 * h]) = pk;
     }
   }
@@ -554,6 +551,7 @@ __global__ __launch_bounds__(256) void chunked_import_kernel(const ChunkParams p
   if ((tid & 63) == 0) wm[tid >> 6] = mw;
   __syncthreads();
   const int eS = exp_of_f32bits(max(max(wm[0], wm[1]), max(wm[2], wm[3])));
+  // the caller's state at any magnitude: the power of two by ldexp on each value (exact and finite)
   const int es = eS == kNoExp ? 0 : 13 - eS;
   if (tid == 0) p.wsE[slot] = eS == kNoExp ? kNoExp : eS - 13;
   for (int idx = tid; idx < 64 * NF; idx += 256)
@@ -607,12 +605,10 @@ __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p
       const u32x2 x0 = *reinterpret_cast<const u32x2*>(base + (size_t)nseg * (64 * NF));
       emax = exg[nseg];
       cnt = 1;
-      if (emax != kNoExp) {
-        acc[0] = __builtin_ldexpf(f16_lo_to_f32(x0[0]), emax);
-        acc[1] = __builtin_ldexpf(f16_hi_to_f32(x0[0]), emax);
-        acc[2] = __builtin_ldexpf(f16_lo_to_f32(x0[1]), emax);
-        acc[3] = __builtin_ldexpf(f16_hi_to_f32(x0[1]), emax);
-      }
+      acc[0] = __builtin_ldexpf(f16_lo_to_f32(x0[0]), emax);
+      acc[1] = __builtin_ldexpf(f16_hi_to_f32(x0[0]), emax);
+      acc[2] = __builtin_ldexpf(f16_lo_to_f32(x0[1]), emax);
+      acc[3] = __builtin_ldexpf(f16_hi_to_f32(x0[1]), emax);
     }
 #pragma unroll
     for (int s0 = 0; s0 < MAX_SEG; s0 += 16) {
@@ -628,17 +624,15 @@ __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p
         emax = max(emax, es);
         ++cnt;
         const int ep = emax == kNoExp ? kNoExp : emax + (cnt > 1 ? 32 - __builtin_clz((unsigned)(cnt - 1)) : 0);
-        // powers of two by ldexp on each value: exact, and finite at any exponent
-        if (es != kNoExp) {
-          acc[0] += __builtin_ldexpf(f16_lo_to_f32(x[i][0]), es);
-          acc[1] += __builtin_ldexpf(f16_hi_to_f32(x[i][0]), es);
-          acc[2] += __builtin_ldexpf(f16_lo_to_f32(x[i][1]), es);
-          acc[3] += __builtin_ldexpf(f16_hi_to_f32(x[i][1]), es);
-        }
-        const int eo = ep == kNoExp ? 0 : -ep;   // acc is zero while ep is kNoExp
+        // powers of two by ldexp on each value: exact, and finite at any exponent (an increment
+        // or prefix with exponent kNoExp is all zeros, which ldexp keeps zero)
+        acc[0] += __builtin_ldexpf(f16_lo_to_f32(x[i][0]), es);
+        acc[1] += __builtin_ldexpf(f16_hi_to_f32(x[i][0]), es);
+        acc[2] += __builtin_ldexpf(f16_lo_to_f32(x[i][1]), es);
+        acc[3] += __builtin_ldexpf(f16_hi_to_f32(x[i][1]), es);
         *reinterpret_cast<u32x2*>(base + (size_t)(s0 + i) * (64 * NF)) =
-            (u32x2){pack_f16x2(__builtin_ldexpf(acc[0], eo), __builtin_ldexpf(acc[1], eo)),
-                    pack_f16x2(__builtin_ldexpf(acc[2], eo), __builtin_ldexpf(acc[3], eo))};
+            (u32x2){pack_f16x2(__builtin_ldexpf(acc[0], -ep), __builtin_ldexpf(acc[1], -ep)),
+                    pack_f16x2(__builtin_ldexpf(acc[2], -ep), __builtin_ldexpf(acc[3], -ep))};
         if (e == 0) p.wsEP[(size_t)bh * p.P + s0 + i] = ep;
       }
     }
@@ -758,6 +752,7 @@ struct SwRole {
   template <class LT>
   __device__ __forceinline__ void prev_v(LT& L, const ChunkParams& p, int c0, int U, int W, int lane) {
     const uint16_t* vh = p.v + hrow * p.dv;
+    const float vs = __builtin_ldexpf(1.0f, -U);
     uint16_t* vt = vtab(L, (c0 + 1) & 1);
 #pragma unroll
     for (int tp = 0; tp < 8; ++tp) {
@@ -765,8 +760,8 @@ struct SwRole {
       const int t = c0 * CH - CH + col;               // its token
       float a = 0.f, b = 0.f;
       if (lane < p.dv && t >= 0) {
-        a = __builtin_ldexpf(bf16_lo_to_f32(vh[(size_t)t * p.dv + lane]), -U);
-        b = __builtin_ldexpf(bf16_lo_to_f32(vh[(size_t)(t + 1) * p.dv + lane]), -U);
+        a = bf16_lo_to_f32(vh[(size_t)t * p.dv + lane]) * vs;
+        b = bf16_lo_to_f32(vh[(size_t)(t + 1) * p.dv + lane]) * vs;
       }
       *reinterpret_cast<u32*>(&vt[vt_off(lane, col >> 3) + (col & 7)]) = pack_f16x2(a, b);
     }
@@ -986,7 +981,7 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
   // softmax role: its slice of the sliding-window branch (queries 32W .. 32W + 31 of each chunk)
   SwRole<DSW> sw;
   if constexpr (LIN) {
-    if (Up != kNoExp && U != Up) acc_scale<NB>(S, Up - U);
+    if (Up != kNoExp && U != Up) acc_scale<NB>(S, __builtin_ldexpf(1.0f, Up - U));
     init_kt_constants(L.KT, tid, 64 * NWAVE_OUT);
     publish_state<NB>(L, S, OB::first, r, h);
     if (GRAM) publish_gram(L, G, r, h);
@@ -994,7 +989,7 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
     if (U == 0)
       stage_convert_v(st, cv);
     else
-      stage_convert_v_scaled(st, cv, -U);
+      stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -U));
     stage_write<true>(cv, L.Q0, L.Kr, L.KT, vtab(L, c0 & 1), lane, W);
     {
       const u32 mvk = wave_max_u16x2((stage_vmax(st) << 16) | stage_kmax(st));
@@ -1018,9 +1013,9 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
     const int U0 = max(Up, first_unit(eVc));
     if (U0 != U) {   // rare, and the same in every wave (both roles)
       if constexpr (LIN) {
-        acc_scale<NB>(S, U - U0);
+        acc_scale<NB>(S, __builtin_ldexpf(1.0f, U - U0));
         publish_state<NB>(L, S, OB::first, r, h);
-        stage_convert_v_scaled(st, cv, -U0);
+        stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -U0));
         stage_write_v(cv, vtab(L, c0 & 1), lane, W);
         if constexpr (LAYER) {
           if (W == 0 && lane == 0) L.Us[c0 & 1] = U0;
@@ -1280,9 +1275,9 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
       const float sb = (eS == kNoExp ? 0.f : __builtin_ldexpf(2.0f, eS)) + dS;
       const int Un = next_unit(U, exp_of_f32bits(__builtin_bit_cast(u32, sb)), eV);
       if (Un != U || (Un != 0 && more)) {   // rare, and the same in every wave
-        if (Un != U) acc_scale<NB>(S, U - Un);
+        if (Un != U) acc_scale<NB>(S, __builtin_ldexpf(1.0f, U - Un));
         if (more) {
-          stage_convert_v_scaled(st, cv, -Un);
+          stage_convert_v_scaled(st, cv, __builtin_ldexpf(1.0f, -Un));
           stage_write_v(cv, vtab(L, (c0 + c + 1) & 1), lane, W);
           if (Un != U) publish_state<NB>(L, S, OB::first, r, h);
         }

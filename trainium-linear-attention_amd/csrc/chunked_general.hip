@@ -44,6 +44,7 @@ struct GParams {
   uint16_t* KV;     // converted chunks [BH][chunks before the last segment][GChunk rows][64]
   u32x2* CE;        // their exponents {Ec, Ez}
   float* Tot;       // per (part < nparts - 1, head, state work-group, thread): its part's sums
+  u32* VM;          // [BH][kVmParts] partial maxima of |v| (bf16 bits) over the prefix tokens
   float* den_out;   // optional (BH, N): each row's denominator without eps
   int nparts, spp;  // the state sweep split into parts of spp segments
   int BH, N, d, dv, nseg, vec;
@@ -87,6 +88,49 @@ struct GChunk {
 };
 
 __device__ __forceinline__ int gswz(int row, int unit) { return (unit ^ ((row >> 1) & 7)) << 3; }
+
+// ---------------------------------------------------------------- head V exponent
+// The prefixes T hold sums of phi(k) v in fp16 beside z = sums of phi(k) with one exponent per
+// (segment, work-group), so V enters them divided by 2^Eh, Eh = floor(log2 max |v|) over the
+// head's tokens before its last segment (the ones the prefixes sum): then T and z keep
+// comparable magnitudes for V of any size (without it, T of a head with |v| ~ 1e-20 would flush
+// to zero beside z), and the output kernel multiplies the inter-segment numerator by 2^Eh.
+constexpr int kVmParts = 64;
+
+// Work-group (part, head): the largest |v| (bf16 bits) of its share of the prefix tokens.
+__global__ __launch_bounds__(256) void gvmax_kernel(const GParams p) {
+  __shared__ u32 wm[4];
+  const int tid = threadIdx.x, s = blockIdx.x, bh = blockIdx.y;
+  const int R = (p.nseg - 1) * GL;                        // prefix tokens (< N)
+  const int per = (R + kVmParts - 1) / kVmParts;
+  const int r0 = min(R, s * per), r1 = min(R, r0 + per);
+  const uint16_t* base = p.v + ((size_t)bh * p.N + r0) * p.dv;
+  const long long n = (long long)(r1 - r0) * p.dv;
+  u32 m = 0u;
+  long long i0 = 0;
+  if ((reinterpret_cast<uintptr_t>(base) & 15) == 0) {   // 16-byte loads over the whole units
+    const u32x4* b4 = reinterpret_cast<const u32x4*>(base);
+    const long long n8 = n / 8;
+    for (long long i = tid; i < n8; i += 256) {
+      const u32x4 x = b4[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) m = max(m, max(x[e] & 0x7fffu, (x[e] >> 16) & 0x7fffu));
+    }
+    i0 = n8 * 8;
+  }
+  for (long long i = i0 + tid; i < n; i += 256) m = max(m, (u32)(base[i] & 0x7fffu));
+  m = wave_max_u32(m);
+  if ((tid & 63) == 0) wm[tid >> 6] = m;
+  __syncthreads();
+  if (tid == 0) p.VM[(size_t)bh * kVmParts + s] = max(max(wm[0], wm[1]), max(wm[2], wm[3]));
+}
+
+// Eh of head bh from its partial maxima (every lane of the wave calls it; the result is uniform).
+__device__ __forceinline__ int head_vexp(const GParams& p, int bh) {
+  const int lane = threadIdx.x & 63;
+  const u32 m = wave_max_u32(p.VM[(size_t)bh * kVmParts + lane]);
+  return m == 0u ? 0 : (int)((m << 16) >> 23) - 127;   // bf16 subnormals: -127
+}
 
 // ---------------------------------------------------------------- kernel 0: chunk conversion
 // One work-group per (head, 64-token chunk) of the tokens before the last segment.  Per token t:
@@ -139,6 +183,11 @@ __global__ __launch_bounds__(256) void gprep_kernel(const GParams p) {
       const int col = part * VPP + e;
       vv[e] = col < dv ? bf16_bits_to_f32(p.v[row * dv + col]) : 0.f;
     }
+  }
+  {
+    const int eh = head_vexp(p, bh);   // V / 2^Eh (exact)
+#pragma unroll
+    for (int e = 0; e < VPP; ++e) vv[e] = __builtin_ldexpf(vv[e], -eh);
   }
   u32 mk = 0u, mv = 0u;
 #pragma unroll
@@ -599,10 +648,11 @@ __global__ __launch_bounds__(256, DVT == 4 ? 1 : 2) void gout_kernel(const GPara
       }
     }
     __syncthreads();   // every wave done with the T stages before the key blocks reuse them
+    const int eh = head_vexp(p, bh);   // the prefixes hold V / 2^Eh
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      const float f = __builtin_ldexpf(m2[nt], emax);
-      den[nt] *= f;
+      den[nt] *= __builtin_ldexpf(m2[nt], emax);
+      const float f = __builtin_ldexpf(m2[nt], emax + eh);
 #pragma unroll
       for (int mt = 0; mt < DVT; ++mt)
 #pragma unroll
@@ -731,7 +781,7 @@ void state_parts(int BH, int nwga, int nseg, int& nparts, int& spp) {
 // (head, chunk before the last segment) the converted chunk and its two exponents; the part
 // totals of the state sweep.
 struct GLayout {
-  size_t t, z, e, kv, ce, tot, total;
+  size_t t, z, e, kv, ce, tot, vm, total;
   int nparts, spp;
 };
 
@@ -757,7 +807,8 @@ GLayout glayout_dp(int BH, int nseg, int DVT) {
   state_parts(BH, FT::NWGA, nseg, L.nparts, L.spp);
   // per state work-group of every part but the last: its eight tiles' sums, 32 x DVT accumulators
   // and a z partial per lane
-  L.total = L.tot + up((size_t)(L.nparts - 1) * BH * FT::NWGA * 512 * (DVT * 16 + 1) * 4);
+  L.vm = L.tot + up((size_t)(L.nparts - 1) * BH * FT::NWGA * 512 * (DVT * 16 + 1) * 4);
+  L.total = L.vm + up((size_t)BH * kVmParts * 4);
   return L;
 }
 
@@ -781,8 +832,11 @@ int launch_g(const GParams& p, hipStream_t stream) {
   using FT = GFeat<DP>;
   if (p.nseg > 1) {
     const int nch = (p.nseg - 1) * (GL / GC);
-    hipLaunchKernelGGL((gprep_kernel<DP, DVT>), dim3((unsigned)(p.BH * nch)), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(gvmax_kernel, dim3((unsigned)kVmParts, (unsigned)p.BH), dim3(256), 0, stream, p);
     int e = (int)hipGetLastError();
+    if (e != 0) return e;
+    hipLaunchKernelGGL((gprep_kernel<DP, DVT>), dim3((unsigned)(p.BH * nch)), dim3(256), 0, stream, p);
+    e = (int)hipGetLastError();
     if (e != 0) return e;
     const unsigned units = (unsigned)(p.BH * FT::NWGA);
     if (p.nparts > 1) {
@@ -865,6 +919,7 @@ int launch_general_chunked(const ChunkedArgs& a, hipStream_t stream) {
     p.KV = reinterpret_cast<uint16_t*>(ws + L.kv);
     p.CE = reinterpret_cast<u32x2*>(ws + L.ce);
     p.Tot = reinterpret_cast<float*>(ws + L.tot);
+    p.VM = reinterpret_cast<u32*>(ws + L.vm);
     p.nparts = L.nparts;
     p.spp = L.spp;
   }

@@ -21,7 +21,7 @@ constexpr int KRS = 136;        // row stride (halves) of the K^T and V^T tables
 constexpr int STS = 168;        // row stride (halves) of S^T: 336 B
 constexpr int KT_ROWS = 20;
 constexpr int R_ONES = 16, R_ZA = 17, R_ZB = 18, R_TWOS = 19;   // constant rows of K^T: 1/2, 0, 0, 1
-constexpr int kNoExp = -128;    // exponent of an all-zero quantity (below every other)
+constexpr int kNoExp = -1024;   // exponent of an all-zero quantity (below every exponent the kernels form)
 
 // ---- feature templates
 //
@@ -215,12 +215,17 @@ __device__ __forceinline__ u32 lds_max4(const u32* x) {
   return (u32)__builtin_amdgcn_readfirstlane((int)max(max(x[0], x[1]), max(x[2], x[3])));
 }
 
+// Lowest unit of V and the state: every factor 2^-U, 2^(U - U') the kernels form stays finite
+// in fp32, and V 2^-U stays in fp16's normal range for every nonzero bf16 v (|v| >= 2^-133).
+constexpr int kMinUnit = -126;
+
 // Exponent of the first chunk from floor(log2 max |v|): 0 while max |v| lies in [2^-6, 2^13)
 // (V^T is then v itself in fp16, without a multiply), else the one that puts max |v| in
-// [2^7, 2^8); an all-zero chunk leaves a placeholder that the first nonzero V raises.
+// [2^7, 2^8), at least kMinUnit; an all-zero chunk takes kMinUnit, which the first nonzero V
+// raises as far as it needs.
 __device__ __forceinline__ int first_unit(int eV) {
-  if (eV == kNoExp) return -200;
-  return (eV >= -6 && eV <= 12) ? 0 : eV - 7;
+  if (eV == kNoExp) return kMinUnit;
+  return (eV >= -6 && eV <= 12) ? 0 : max(eV - 7, kMinUnit);
 }
 
 
