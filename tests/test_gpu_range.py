@@ -271,3 +271,42 @@ def test_general_v_tiny_prefix():
     errs = head_errs(_run("chunked", q, k, v), want)
     print("general d64 tiny-V prefix errs " + " ".join(f"{x:.2e}" for x in errs))
     assert max(errs) < TOL
+
+
+@pytest.mark.parametrize("vscale", [1e-36, 1e30])
+def test_v_extreme_scales_other_paths(vscale):
+    """The same V scales on the fp32 segment-state path (d 16 and 64, fp32 bar), the identity
+    map, the one-launch layer (bf16 output: max |y - y_ref| / (|y_ref| + rms)) and a decode step
+    after a prefill."""
+    from tests.helpers import rounded_err
+    K = _kernels()
+    for d in (16, 64):
+        q, k, v = rand_qkv(1, 2, 1500, d, 64, seed=4, dtype=torch.float32, scale_qk=0.5)
+        v = v * vscale
+        want, _, _ = ref.based_dense(q, k, v)
+        e = max(head_errs(K.based_chunked(*to_dev(q, k, v), out_dtype=torch.float32), want))
+        print(f"fp32 segment-state d={d} v x {vscale:g}: err={e:.3e}")
+        assert e < TOL_F32
+    q, k, v = _scaled(1, 2, 1000, 16, 64, seed=5, vscale=vscale)
+    y = K.identity_linear_attn(*to_dev(q, k, v), out_dtype=torch.float32)
+    e = max(head_errs(y, ref.ref_identity_numerator(q.double(), k.double(), v.double())))
+    print(f"identity v x {vscale:g}: err={e:.3e}")
+    assert e < 1e-3
+    q, k, v = _scaled(2, 4, 2600, 16, 64, seed=6, vscale=vscale)
+    g = torch.Generator().manual_seed(7)
+    qs = (torch.randn(2, 4, 2600, 16, generator=g) * 0.5).bfloat16()
+    ks = (torch.randn(2, 4, 2600, 16, generator=g) * 0.5).bfloat16()
+    y = K.based_layer_attn(*to_dev(q, k, v, qs, ks)[:3], window_size=64, q_sw=qs.cuda(), k_sw=ks.cuda())
+    want = ref.based_layer_dense(q[:, :1], k[:, :1], v[:, :1], window_size=64, q_sw=qs[:, :1], k_sw=ks[:, :1])
+    e = rounded_err(y.float()[:, :1], want)
+    print(f"layer v x {vscale:g}: err={e:.3e}")
+    assert torch.isfinite(y).all() and e < TOL
+    q, k, v = _scaled(1, 2, 301, 16, 64, seed=8, vscale=vscale)
+    qd, kd, vd = to_dev(q, k, v)
+    _, st = K.based_chunked(qd[:, :, :300], kd[:, :, :300], vd[:, :, :300], out_dtype=torch.float32,
+                            return_state=True)
+    yd = K.based_decode_step(qd[:, :, 300:], kd[:, :, 300:], vd[:, :, 300:], st).float().cpu()
+    want, _, _ = ref.based_dense(q, k, v)
+    e = rounded_err(yd[:, :, 0], want[:, :, 300])
+    print(f"decode after prefill v x {vscale:g}: err={e:.3e}")
+    assert torch.isfinite(yd).all() and e < TOL
