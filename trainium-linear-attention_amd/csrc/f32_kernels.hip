@@ -655,20 +655,21 @@ __global__ __launch_bounds__(512, 2) void f32_x6_split_kernel(const F32Params p)
       for (int r = 0; r < 3; ++r) qf[r][c] = a.t[r];
     }
   }
-#pragma unroll 1
+  // every tile's loads first (the K rows, then the V elements), so that the second tile's data is
+  // in flight during the first tile's products
+  float xk[X6_TPW][8], xv[X6_TPW][MT][2][8];
+#pragma unroll
   for (int j = 0; j < X6_TPW; ++j) {
     const int u = TP * part + w + NW * j;   // this wave's key tile
-    if (u > ud) break;
     const int kb = KT * u;
-    // all loads of the tile first: the K row (two 16-byte loads), then the V elements
-    float xk[8], xv[MT][2][8];
+    const bool live = u <= ud;
 #pragma unroll
     for (int e = 0; e < 8; e += 4) {
       const int col = 8 * h + e;
       f32x4 tk = {0.f, 0.f, 0.f, 0.f};
-      if (kb + n < N && col < d) tk = *reinterpret_cast<const f32x4*>(kg + (size_t)(kb + n) * d + col);
+      if (live && kb + n < N && col < d) tk = *reinterpret_cast<const f32x4*>(kg + (size_t)(kb + n) * d + col);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xk[e + i] = tk[i];
+      for (int i = 0; i < 4; ++i) xk[j][e + i] = tk[i];
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -677,12 +678,18 @@ __global__ __launch_bounds__(512, 2) void f32_x6_split_kernel(const F32Params p)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int key = kb + 16 * m + 8 * (e >> 2) + 4 * h + (e & 3), col = 32 * mt + n;
-          xv[mt][m][e] = (key < N && col < dv) ? vg[(size_t)key * dv + col] : 0.f;
+          xv[j][mt][m][e] = (live && key < N && col < dv) ? vg[(size_t)key * dv + col] : 0.f;
         }
+  }
+#pragma unroll
+  for (int j = 0; j < X6_TPW; ++j) {
+    const int u = TP * part + w + NW * j;
+    if (u > ud) break;
+    const int kb = KT * u;
     u32x4 kf[3];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const Split3 b = split3_bf16x2(xk[2 * c], xk[2 * c + 1]);
+      const Split3 b = split3_bf16x2(xk[j][2 * c], xk[j][2 * c + 1]);
 #pragma unroll
       for (int r = 0; r < 3; ++r) kf[r][c] = b.t[r];
     }
@@ -711,7 +718,7 @@ __global__ __launch_bounds__(512, 2) void f32_x6_split_kernel(const F32Params p)
         u32x4 vf[3];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const Split3 s3 = split3_bf16x2(xv[mt][m][2 * c], xv[mt][m][2 * c + 1]);
+          const Split3 s3 = split3_bf16x2(xv[j][mt][m][2 * c], xv[j][mt][m][2 * c + 1]);
 #pragma unroll
           for (int r = 0; r < 3; ++r) vf[r][c] = s3.t[r];
         }
