@@ -47,15 +47,20 @@ __device__ __forceinline__ int vexp_step(u32 absmax_f32_bits) {
 }
 
 // One work-group per PPW consecutive 64-key blocks of a head (all their loads issued first); k
-// rows are d = 16 bf16 (16-byte aligned), v rows dv % 8 == 0 bf16 (8-byte aligned).  Per block:
+// rows are d = 16 bf16 (16-byte aligned), v rows dv % 8 == 0 bf16 (8-byte aligned).  Loads go
+// through raw buffer resources over the head's rows, so rows past N (and columns past dv) read
+// as zero without per-lane branches.  Per block:
 //  * V^T: thread t takes keys 2 (t / CPR) and 2 (t / CPR) + 1, columns 8 (t % CPR) .. +7, so it
 //    holds both halves of 8 fp16 pairs of the transposed block; it writes them into an LDS
 //    image of the block (padding zero), which whole-chunk stores then copy out;
-//  * column sums of V from the same registers: lane shuffles, then the waves through LDS;
+//  * column sums of V from the same registers: a butterfly over the lanes of one column group
+//    (each exchange halves the columns a lane carries, 7 shuffles for 8 columns), then the
+//    waves through LDS;
 //  * k sums and the k k^T triangle from one 32x32x16 MFMA chain over the 64 keys (wave 0):
 //    A = K^T (rows 16..31 zero), B = K with a column of ones at 16, so C[a][b] = (k k^T)[a][b]
-//    and C[a][16] = k1[a].
+//    and C[a][16] = k1[a]; K^T sits in LDS as rows of keys, so each operand is one 16-byte read.
 constexpr int PPW = 1;   // blocks per pack work-group
+constexpr int KTS = BN + 8;   // K^T row stride (halves): 144 bytes, the operand reads on distinct banks
 
 template <int DV, int ROW>
 __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -66,15 +71,17 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
   constexpr int NT = (BN / 2) * CPR;          // threads holding a (key pair, column group)
   constexpr int NWV = NT / 64;                // waves among them
   constexpr int IMG = VtBlock<DV, ROW>::bytes;
-  static_assert(ROW % 2 == 0 && NT <= 256, "pack layout");
+  static_assert(ROW % 2 == 0 && NT <= 256 && (CPR == 4 || CPR == 8), "pack layout");
   __shared__ __attribute__((aligned(16))) u32 img[IMG / 4];
-  __shared__ __attribute__((aligned(16))) uint16_t kl[BN * 16];
+  __shared__ __attribute__((aligned(16))) uint16_t kt[16 * KTS];
   __shared__ float csum[NWV][DV];
   __shared__ u32 vmx[4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int bh = blockIdx.y, blk0 = blockIdx.x * PPW;
   const int nb = min(PPW, nb64 - blk0);
   const int kp = tid / CPR, cg = tid % CPR, col = 8 * cg;
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(v + (size_t)bh * N * dv, (u32)N * (u32)dv * 2u);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(k + (size_t)bh * N * 16, (u32)N * 32u);
 
   for (int i = tid; i < IMG / 16; i += 256) reinterpret_cast<u32x4*>(img)[i] = (u32x4){0u, 0u, 0u, 0u};
 
@@ -82,24 +89,14 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
 #pragma unroll
   for (int b = 0; b < PPW; ++b) {
     const int row0 = (blk0 + b) * BN;
-    u32x4 x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
-    if (b < nb && tid < NT && col < dv) {
-      const uint16_t* src = v + ((size_t)bh * N + row0 + 2 * kp) * dv + col;
-      if (row0 + 2 * kp < N) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(src), hi = *reinterpret_cast<const u32x2*>(src + 4);
-        x0 = (u32x4){lo[0], lo[1], hi[0], hi[1]};
-      }
-      if (row0 + 2 * kp + 1 < N) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(src + dv), hi = *reinterpret_cast<const u32x2*>(src + dv + 4);
-        x1 = (u32x4){lo[0], lo[1], hi[0], hi[1]};
-      }
-    }
-    va[b] = x0;
-    vb[b] = x1;
-    u32x4 y = {0u, 0u, 0u, 0u};
-    if (b < nb && tid < 128 && row0 + (tid >> 1) < N)
-      y = *reinterpret_cast<const u32x4*>(k + ((size_t)bh * N + row0 + (tid >> 1)) * 16 + 8 * (tid & 1));
-    kx[b] = y;
+    // rows past N read zero through the resource; threads past NT and columns past dv read
+    // nothing (an offset out of range)
+    const int vo = (b < nb && tid < NT && col < dv) ? ((row0 + 2 * kp) * dv + col) * 2 : kOffOutOfRange;
+    const u32x2 a0 = buf_load_b64(rv, vo), a1 = buf_load_b64(rv, vo + 8);
+    const u32x2 b0 = buf_load_b64(rv, vo + 2 * dv), b1 = buf_load_b64(rv, vo + 2 * dv + 8);
+    va[b] = (u32x4){a0[0], a0[1], a1[0], a1[1]};
+    vb[b] = (u32x4){b0[0], b0[1], b1[0], b1[1]};
+    kx[b] = buf_load_b128(rk, (b < nb && tid < 128) ? (row0 + (tid >> 1)) * 32 + 16 * (tid & 1) : kOffOutOfRange);
   }
 
 #pragma unroll
@@ -121,29 +118,49 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
     // fp16(v 2^-eb) by ldexp on each value: exact, and finite for an all-zero block (eb = -128)
     const int eb = vexp_step(max(max(vmx[0], vmx[1]), max(vmx[2], vmx[3])) << 16);
     float part[8];
-    if (tid < NT) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const u32 a0 = va[b][e >> 1], a1 = vb[b][e >> 1];
-        const float f0 = (e & 1) ? bf16_hi_to_f32(a0) : bf16_lo_to_f32(a0);
-        const float f1 = (e & 1) ? bf16_hi_to_f32(a1) : bf16_lo_to_f32(a1);
-        part[e] = f0 + f1;
+    for (int e = 0; e < 8; ++e) {
+      const u32 a0 = va[b][e >> 1], a1 = vb[b][e >> 1];
+      const float f0 = (e & 1) ? bf16_hi_to_f32(a0) : bf16_lo_to_f32(a0);
+      const float f1 = (e & 1) ? bf16_hi_to_f32(a1) : bf16_lo_to_f32(a1);
+      part[e] = f0 + f1;   // zero for threads past NT (they loaded nothing)
+      if (tid < NT)
         img[(col + e) * (ROW / 2) + kp] = pack_f16x2(__builtin_ldexpf(f0, -eb), __builtin_ldexpf(f1, -eb));
+    }
+    // K^T: thread t < 128 holds dims 8 (t & 1) .. +7 of key t / 2
+    if (tid < 128) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        kt[(8 * (tid & 1) + 2 * j) * KTS + (tid >> 1)] = (uint16_t)(kx[b][j] & 0xffffu);
+        kt[(8 * (tid & 1) + 2 * j + 1) * KTS + (tid >> 1)] = (uint16_t)(kx[b][j] >> 16);
       }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) part[e] = 0.f;
     }
-    if (tid < 128) *reinterpret_cast<u32x4*>(&kl[8 * tid]) = kx[b];
-    // column sums: lanes with the same column group differ by multiples of CPR
+    // column sums over the lanes of this column group (lane bits log2(CPR) .. 5): each exchange
+    // keeps the half of the lane's columns that its bit selects and adds the partner's copy of
+    // them, so that after three exchanges a lane holds one column's sum over 8 lanes (CPR = 8);
+    // with CPR = 4 a fourth exchange adds the other half of the wave
+    float p4[4], p2[2];
+    {
+      const bool up = (lane & CPR) != 0;
 #pragma unroll
-    for (int sh = CPR; sh < 64; sh <<= 1)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) part[e] += __shfl_xor(part[e], sh);
-    if (w < NWV && lane < CPR) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) csum[w][8 * lane + e] = part[e];
+      for (int i = 0; i < 4; ++i)
+        p4[i] = (up ? part[4 + i] : part[i]) + __shfl_xor(up ? part[i] : part[4 + i], CPR);
     }
+    {
+      const bool up = (lane & (2 * CPR)) != 0;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        p2[i] = (up ? p4[2 + i] : p4[i]) + __shfl_xor(up ? p4[i] : p4[2 + i], 2 * CPR);
+    }
+    float p1;
+    {
+      const bool up = (lane & (4 * CPR)) != 0;
+      p1 = (up ? p2[1] : p2[0]) + __shfl_xor(up ? p2[0] : p2[1], 4 * CPR);
+    }
+    if (CPR == 4) p1 += __shfl_xor(p1, 32);
+    // lane's column: col + 4 (bit CPR) + 2 (bit 2 CPR) + (bit 4 CPR)
+    const int sc = col + ((lane & CPR) ? 4 : 0) + ((lane & (2 * CPR)) ? 2 : 0) + ((lane & (4 * CPR)) ? 1 : 0);
+    if (w < NWV && (CPR == 8 || lane < 32)) csum[w][sc] = p1;
     __syncthreads();
     u32* dst = reinterpret_cast<u32*>(vt + ((size_t)bh * nb64 + blk) * (IMG / 2));
     for (int i = tid; i < IMG / 16; i += 256) reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(img)[i];
@@ -159,16 +176,9 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
       f32x16 acc = splat16(0.f);
 #pragma unroll
       for (int k0 = 0; k0 < BN; k0 += 16) {
-        u32 av[4], bv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = k0 + 8 * h + 2 * i;
-          const int c = nn < 16 ? nn : 0;
-          const u32 x0 = kl[key * 16 + c], x1 = kl[(key + 1) * 16 + c];
-          av[i] = nn < 16 ? (x0 | (x1 << 16)) : 0u;
-          bv[i] = nn == 16 ? 0x3f803f80u : av[i];   // bf16 (1, 1)
-        }
-        acc = mfma32x32x16((u32x4){av[0], av[1], av[2], av[3]}, (u32x4){bv[0], bv[1], bv[2], bv[3]}, acc);
+        const u32x4 x = nn < 16 ? *reinterpret_cast<const u32x4*>(&kt[nn * KTS + k0 + 8 * h]) : (u32x4){0u, 0u, 0u, 0u};
+        const u32 one = nn == 16 ? 0x3f803f80u : 0u;   // bf16 (1, 1)
+        acc = mfma32x32x16(x, nn < 16 ? x : (u32x4){one, one, one, one}, acc);
       }
       // lane: column nn, rows c32_row(i, h) (< 16 for i < 8)
 #pragma unroll
