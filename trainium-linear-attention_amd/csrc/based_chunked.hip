@@ -101,7 +101,7 @@ struct LayerLds {
   int eg;
   int Us[2];
   uint16_t KSW[2][CH * (DSW + 8)];
-  __attribute__((aligned(16))) float YL[CH * YLS];
+  float YL[CH * YLS];
 };
 __device__ __forceinline__ uint16_t* vtab(OutLds& L, int) { return L.VT; }
 template <int DSW>
@@ -866,39 +866,21 @@ struct SwRole {
     const int r = lane & 31, h = lane >> 5, qs = 32 * W, row0 = cabs * CH, dv = p.dv;
     const __amdgpu_buffer_rsrc_t ro =
         make_rsrc(static_cast<char*>(p.out) + (hrow + row0) * dv * esz, (u32)(p.N - row0) * (u32)dv * (u32)esz);
-    // The wave's rows of the linear branch first, then the sums staged in those same LDS rows
-    // (only this wave touches them until the next barrier; 16-byte units XOR-swizzled by row) and
-    // stored as whole line pieces by consecutive lanes, non-temporal.
-    f32x4 yl[2][4];
-#pragma unroll
-    for (int n = 0; n < 2; ++n)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) yl[n][jj] = *reinterpret_cast<const f32x4*>(&L.YL[(qs + r) * YLS + 32 * n + 8 * jj + 4 * h]);
-    asm volatile("" ::: "memory");   // every read above before the staging writes below
-    constexpr int RB = 64 * esz, UR = RB / 16;   // staged row bytes (dv <= 64), 16-byte units per row
-    static_assert(32 * RB <= 32 * YLS * 4, "staging fits the wave's rows");
-    char* stg = reinterpret_cast<char*>(&L.YL[qs * YLS]);
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
+        const int col = 32 * n + 8 * jj + 4 * h;
+        const f32x4 yl = *reinterpret_cast<const f32x4*>(&L.YL[(qs + r) * YLS + col]);
         float y[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = yl[n][jj][e] + O[n][4 * jj + e] * ysc;
-        const int cb = (32 * n + 8 * jj + 4 * h) * esz, u = cb >> 4;
-        char* dst = stg + r * RB + 16 * (u ^ (r & (UR - 1))) + (cb & 15);
+        for (int e = 0; e < 4; ++e) y[e] = yl[e] + O[n][4 * jj + e] * ysc;
+        const int voff = col < dv ? ((qs + r) * dv + col) * esz : kOffOutOfRange;
         if (OUT_F32)
-          *reinterpret_cast<f32x4*>(dst) = (f32x4){y[0], y[1], y[2], y[3]};
+          buf_store_b128(__builtin_bit_cast(u32x4, (f32x4){y[0], y[1], y[2], y[3]}), ro, voff);
         else
-          *reinterpret_cast<u32x2*>(dst) = (u32x2){pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+          buf_store_b64((u32x2){pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])}, ro, voff);
       }
-    }
-    // (LDS operations of one wave complete in order: the reads below see the writes above)
-#pragma unroll
-    for (int i = 0; i < 32 * UR / 64; ++i) {
-      const int idx = 64 * i + lane, row = idx / UR, u = idx % UR;
-      const u32x4 x = *reinterpret_cast<const u32x4*>(stg + row * RB + 16 * (u ^ (row & (UR - 1))));
-      buf_store_b128_nt(x, ro, 16 * u < dv * esz ? (qs + row) * dv * esz + 16 * u : kOffOutOfRange);
     }
     if (more) {
       store_k(L, cabs + 1, W, lane);
