@@ -372,54 +372,23 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 8
         }
       }
     }
-  }
-  // Outputs.  bf16 without an addend (the plain call): each wave parks its 32 rows, rounded, in
-  // the freed V rows (16-byte units XOR-swizzled by row) and stores them as whole 128-byte line
-  // pieces, eight lanes per line, with the non-temporal hint (no dirty L2 lines for the kernel's
-  // end to write back).  fp32 or with an addend: per-lane pieces as before.
-  constexpr int UR = DV / 8;   // 16-byte bf16 units per row
-  static_assert(NW * 32 * DV <= kResBlocks * BN * DV && (UR & (UR - 1)) == 0, "output staging fits");
-  const bool staged = !p.out_f32 && p.addend == nullptr;
-  if (staged) __syncthreads();   // every wave is done with the K / V rows (uniform condition)
-  if (wave_live) {
-    const float inv = 1.0f / (lrun + __shfl_xor(lrun, 32));
-    if (staged) {
-      uint16_t* ost = &Vl[0][0] + w * (32 * DV);
+    const float lt = lrun + __shfl_xor(lrun, 32);
+    const int query = wq0 + n;
+    if (query < N) {
+      const float inv = 1.0f / lt;
+      const size_t obase = (hrow + query) * (size_t)DV;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int u = 4 * mt + g;
-          *reinterpret_cast<u32x2*>(&ost[n * DV + 8 * (u ^ (n & (UR - 1))) + 4 * h]) =
-              (u32x2){pack_bf16x2(acc[mt][4 * g] * inv, acc[mt][4 * g + 1] * inv),
-                      pack_bf16x2(acc[mt][4 * g + 2] * inv, acc[mt][4 * g + 3] * inv)};
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = acc[mt][4 * g + e] * inv;
+          store_out4<true>(p.out, p.out_f32, obase, 32 * mt + 8 * g + 4 * h, DV, y, p.addend);
         }
-      // (LDS operations of one wave complete in order: its reads below see its writes)
-#pragma unroll
-      for (int i = 0; i < 32 * UR / 64; ++i) {
-        const int idx = 64 * i + lane, row = idx / UR, u = idx % UR;
-        if (wq0 + row >= N) continue;
-        const u32x4 x = *reinterpret_cast<const u32x4*>(&ost[row * DV + 8 * (u ^ (row & (UR - 1)))]);
-        __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.out) + (hrow + wq0 + row) * (size_t)DV + 8 * u));
-      }
-    } else {
-      const int query = wq0 + n;
-      if (query < N) {
-        const size_t obase = (hrow + query) * (size_t)DV;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            float y[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = acc[mt][4 * g + e] * inv;
-            store_out4<true>(p.out, p.out_f32, obase, 32 * mt + 8 * g + 4 * h, DV, y, p.addend);
-          }
-      }
     }
   }
 }
-
 
 template <int KS, int MT, int QT>
 int launch_sl(SlidingParams p, bool vec, hipStream_t stream) {
