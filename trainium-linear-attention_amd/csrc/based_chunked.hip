@@ -499,30 +499,14 @@ __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_k
   const int es = eS == kNoExp ? 0 : min(13 - eS, 127);
   const int EI = eS == kNoExp ? kNoExp : Uo - es;
   const float f = eS == kNoExp ? 0.f : __builtin_ldexpf(1.0f, es);
-  // S^T rows staged in LDS behind the Gram partials (rows of SSR halves, padded against bank
-  // conflicts), then stored as whole lines by consecutive threads, non-temporal (the record is
-  // read by the next kernel only)
-  constexpr int SSR = NF + 8;
-  uint16_t* stg = reinterpret_cast<uint16_t*>(red + NWAVE_SEG * 64 * 16);
-  static_assert(sizeof(float) * NWAVE_SEG * 64 * 16 + 2 * 64 * SSR <= sizeof(SegLds), "staging fits");
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
+  for (int n = 0; n < (active ? 2 : 0); ++n) {
 #pragma unroll
     for (int J = 0; J < 2; ++J) {
       const f32x16& a = S[0][n];
       const u32x4 pk = {pack_f16x2(a[8 * J + 0] * f, a[8 * J + 1] * f), pack_f16x2(a[8 * J + 2] * f, a[8 * J + 3] * f),
                         pack_f16x2(a[8 * J + 4] * f, a[8 * J + 5] * f), pack_f16x2(a[8 * J + 6] * f, a[8 * J + 7] * f)};
-      *reinterpret_cast<u32x4*>(&stg[(32 * n + r) * SSR + 32 * w + 16 * J + 8 * h]) = pk;
-    }
-  }
-  lds_barrier();
-  if (active) {
-    constexpr int UR = NF / 8;   // 16-byte units per row
-#pragma unroll
-    for (int i = 0; i < 64 * UR / (64 * NWAVE_SEG); ++i) {
-      const int u = tid + 64 * NWAVE_SEG * i, row = u / UR, c = u - row * UR;
-      __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&stg[row * SSR + 8 * c]),
-                                  reinterpret_cast<u32x4*>(ws) + u);
+      *reinterpret_cast<u32x4*>(&ws[(32 * n + r) * NF + 32 * w + 16 * J + 8 * h]) = pk;
     }
   }
   if (w == 0 && lane == 0 && active) p.wsE[slot] = EI;
@@ -533,7 +517,7 @@ __global__ __launch_bounds__(64 * NWAVE_SEG * SEG_PER_WG) void chunked_segment_k
       f32x4 acc = *reinterpret_cast<const f32x4*>(&red[lane * 16 + e]);
 #pragma unroll
       for (int ww = 1; ww < NWAVE_SEG; ++ww) acc += *reinterpret_cast<const f32x4*>(&red[(ww * 64 + lane) * 16 + e]);
-      __builtin_nontemporal_store(acc, reinterpret_cast<f32x4*>(&gout[e]));
+      *reinterpret_cast<f32x4*>(&gout[e]) = acc;
     }
   }
 }
