@@ -630,10 +630,9 @@ __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p
         acc[1] += __builtin_ldexpf(f16_hi_to_f32(x[i][0]), es);
         acc[2] += __builtin_ldexpf(f16_lo_to_f32(x[i][1]), es);
         acc[3] += __builtin_ldexpf(f16_hi_to_f32(x[i][1]), es);
-        // non-temporal: read by the next kernel only (consecutive threads fill whole lines)
-        __builtin_nontemporal_store((u32x2){pack_f16x2(__builtin_ldexpf(acc[0], -ep), __builtin_ldexpf(acc[1], -ep)),
-                                            pack_f16x2(__builtin_ldexpf(acc[2], -ep), __builtin_ldexpf(acc[3], -ep))},
-                                    reinterpret_cast<u32x2*>(base + (size_t)(s0 + i) * (64 * NF)));
+        *reinterpret_cast<u32x2*>(base + (size_t)(s0 + i) * (64 * NF)) =
+            (u32x2){pack_f16x2(__builtin_ldexpf(acc[0], -ep), __builtin_ldexpf(acc[1], -ep)),
+                    pack_f16x2(__builtin_ldexpf(acc[2], -ep), __builtin_ldexpf(acc[3], -ep))};
         if (e == 0) p.wsEP[(size_t)bh * p.P + s0 + i] = ep;
       }
     }
@@ -649,7 +648,7 @@ __global__ __launch_bounds__(256) void chunked_prefix_kernel(const ChunkParams p
       for (int i = 0; i < 16; ++i) {
         if (s0 + i >= nseg) break;
         acc += x[i];
-        __builtin_nontemporal_store(acc, reinterpret_cast<f32x2*>(base + (size_t)(s0 + i) * 1024));
+        *reinterpret_cast<f32x2*>(base + (size_t)(s0 + i) * 1024) = acc;
       }
     }
   }
@@ -1197,7 +1196,7 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
             for (int i = 0; i < 4; ++i) {
               const int row = 8 * i + rr, col = 32 * n + 4 * cu;
               const u32x4 x = *reinterpret_cast<const u32x4*>(&os[ost_off(row, cu)]);
-              buf_store_b128_nt(x, ro, col < dv ? ((32 * W + row) * dv + col) * 4 : kOffOutOfRange);
+              buf_store_b128(x, ro, col < dv ? ((32 * W + row) * dv + col) * 4 : kOffOutOfRange);
             }
           }
         } else {
@@ -1212,7 +1211,7 @@ __device__ __forceinline__ void output_wave(LT& L, const ChunkParams& p, int bh,
           for (int i = 0; i < 4; ++i) {
             const int row = 8 * i + rr, col = 8 * cu;
             const u32x4 x = *reinterpret_cast<const u32x4*>(&os[ost_off(row, cu)]);
-            buf_store_b128_nt(x, ro, col < dv ? ((32 * W + row) * dv + col) * 2 : kOffOutOfRange);
+            buf_store_b128(x, ro, col < dv ? ((32 * W + row) * dv + col) * 2 : kOffOutOfRange);
           }
         }
       } else if (row < N) {

@@ -679,8 +679,7 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
       for (int it = 0; it < CPR * QT / 2; ++it) {   // the wave's 32 QT rows, no more
         const int idx = 64 * it + lane, r = idx / CPR, c = idx % CPR;
         const u32x4 x = *reinterpret_cast<const u32x4*>(tile + r * RS + 16 * c);
-        if (wq0 + r < N && 16 * c < rowbytes)   // non-temporal: final output, streamed past L2
-          __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(out + (size_t)r * rowbytes + 16 * c));
+        if (wq0 + r < N && 16 * c < rowbytes) *reinterpret_cast<u32x4*>(out + (size_t)r * rowbytes + 16 * c) = x;
       }
     };
     if (p.out_f32)

@@ -197,18 +197,5 @@ __device__ __forceinline__ void buf_store_b128(u32x4 x, __amdgpu_buffer_rsrc_t r
   typedef __attribute__((__vector_size__(4 * sizeof(u32)))) u32 v4;
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4, x), r, voff, 0, 0);
 }
-// Stores of a kernel's final outputs (no later read in the same kernel) as whole 128-byte lines
-// carry the non-temporal hint (cache policy nt): they stream to memory instead of leaving dirty
-// lines in the XCD's L2, which the end of every kernel would otherwise write back before the next
-// one starts.  Only for whole lines: scattered 8- and 16-byte pieces with the hint measured 2.7x
-// slower (the sliding-window kernel's stores), so those stay plain.
-__device__ __forceinline__ void buf_store_b64_nt(u32x2 x, __amdgpu_buffer_rsrc_t r, int voff) {
-  typedef __attribute__((__vector_size__(2 * sizeof(u32)))) u32 v2;
-  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2, x), r, voff, 0, 2);
-}
-__device__ __forceinline__ void buf_store_b128_nt(u32x4 x, __amdgpu_buffer_rsrc_t r, int voff) {
-  typedef __attribute__((__vector_size__(4 * sizeof(u32)))) u32 v4;
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4, x), r, voff, 0, 2);
-}
 
 }  // namespace la

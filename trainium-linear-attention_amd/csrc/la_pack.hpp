@@ -163,10 +163,7 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
     if (w < NWV && (CPR == 8 || lane < 32)) csum[w][sc] = p1;
     __syncthreads();
     u32* dst = reinterpret_cast<u32*>(vt + ((size_t)bh * nb64 + blk) * (IMG / 2));
-    // non-temporal: the blocks are read by the next kernel, not by this one (no dirty L2 lines
-    // left for the end of the kernel to write back)
-    for (int i = tid; i < IMG / 16; i += 256)
-      __builtin_nontemporal_store(reinterpret_cast<const u32x4*>(img)[i], reinterpret_cast<u32x4*>(dst) + i);
+    for (int i = tid; i < IMG / 16; i += 256) reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(img)[i];
     float* __restrict__ rec = stats + ((size_t)bh * nb64 + blk) * SW;
     if (tid < DV) {
       float t = 0.f;
