@@ -81,6 +81,7 @@ struct ParallelParams {
   u32 ones_hi, ones_lo;   // fp16 bits of the weight W of "1" in u units, hi + lo (both halves)
   const u32* vmax;        // register-staged bf16 path: per head, VR partial maxima of |v| (bf16 bits)
   int normalize, out_f32;
+  int xcd_cus;            // CUs per XCD (the work-group order of the 256-query packed kernel)
 };
 
 constexpr int VR = 64;    // partial maxima of |v| per head (vrange_kernel)
@@ -130,7 +131,8 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
   const int N = p.N, d = p.d, dv = p.dv;
 
   int bh, qb;
-  map_causal_block(blockIdx.x, p.BH, p.nqb, bh, qb);
+  // 256-query packed work-groups (two per CU at dv > 32): first round paired by size
+  map_causal_block(blockIdx.x, p.BH, p.nqb, bh, qb, (PACKED && QT == 2 && MT == 2) ? p.xcd_cus : 0);
   const int q0 = qb * BM;
   const int jb0 = q0 / BN;
   const int nblk = min((N + BN - 1) / BN, (q0 + BM) / BN);
@@ -855,6 +857,7 @@ int launch_based_parallel(const ParallelArgs& a, hipStream_t stream) {
   p.N = a.N;
   p.d = a.d;
   p.dv = a.dv;
+  p.xcd_cus = device_cu_count() / 8;
   // Work in u'' = 2^-2k u with u = (q.k + 1/c)^2 - 1/c^2 = (2/c^2) r, k chosen so that the weight
   // of "1", W = 2^-2k * 2/c^2, lies in (0.18, 0.71] (u'' = W r): r up to 65504 / W stays inside
   // fp16 (|s| up to ~430, 511 at scale = 1/4, where W = 1/2 and 1/c scales to 1/2).
