@@ -50,6 +50,7 @@ struct GParams {
   int BH, N, d, dv, nseg, vec;
   float scale, eps;
   int normalize, out_f32;
+  int alt_prio;     // state kernel: more work-groups than CUs (two share a CU), alternate priorities
 };
 
 constexpr u32 kOnesBf16 = 0x3f803f80u;
@@ -364,6 +365,16 @@ __global__ __launch_bounds__(64 * (8 / TW), TW == 1 ? 4 : 1) void gstate_kernel(
   }
   for (int c = c0; c < c0 + NS - 1; ++c) issue(c);
   for (int gc = c0; gc < c1; ++gc) {
+    // Of two work-groups on one CU the older one's waves issue first at equal priority and the
+    // younger one fell behind, then ran alone.  Priority 1 at even chunks and 0 at odd ones
+    // alternates the lead, so their progress stays within about a chunk (B2 H16 N8192 d64
+    // 444 -> 424 us, N16384 886 -> 863 us in one process; no change where each CU holds one).
+    if (p.alt_prio) {
+      if ((gc - c0) & 1)
+        __builtin_amdgcn_s_setprio(0);
+      else
+        __builtin_amdgcn_s_setprio(1);
+    }
     // this wave's copies of chunk gc landed (later chunks may still be in flight), then every
     // wave's; every wave is also done with chunk gc - 1, whose stage the next copy reuses
     wait_vm(my_units * min(NS - 2, c1 - 1 - gc));
@@ -839,14 +850,18 @@ int launch_g(const GParams& p, hipStream_t stream) {
     e = (int)hipGetLastError();
     if (e != 0) return e;
     const unsigned units = (unsigned)(p.BH * FT::NWGA);
+    const long long cus = device_cu_count();
+    GParams ps = p;
     if (p.nparts > 1) {
+      ps.alt_prio = (long long)units * (p.nparts - 1) > cus ? 1 : 0;
       hipLaunchKernelGGL((gstate_kernel<DP, DVT, true, state_tw<DVT>()>), dim3(units * (unsigned)(p.nparts - 1)),
-                         dim3(64 * (8 / state_tw<DVT>())), 0, stream, p);
+                         dim3(64 * (8 / state_tw<DVT>())), 0, stream, ps);
       e = (int)hipGetLastError();
       if (e != 0) return e;
     }
+    ps.alt_prio = (long long)units * p.nparts > cus ? 1 : 0;
     hipLaunchKernelGGL((gstate_kernel<DP, DVT, false, state_tw<DVT>()>), dim3(units * (unsigned)p.nparts),
-                       dim3(64 * (8 / state_tw<DVT>())), 0, stream, p);
+                       dim3(64 * (8 / state_tw<DVT>())), 0, stream, ps);
     e = (int)hipGetLastError();
     if (e != 0) return e;
   }
