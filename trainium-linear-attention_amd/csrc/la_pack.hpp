@@ -114,9 +114,37 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
       m = wave_max_u32(m);
       if (lane == 0) vmx[w] = m;
     }
-    __syncthreads();   // image zeroed / the previous block's readers done / wave maxima written
+    // K^T: thread t < 128 holds dims 8 (t & 1) .. +7 of key t / 2
+    if (tid < 128) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        kt[(8 * (tid & 1) + 2 * j) * KTS + (tid >> 1)] = (uint16_t)(kx[b][j] & 0xffffu);
+        kt[(8 * (tid & 1) + 2 * j + 1) * KTS + (tid >> 1)] = (uint16_t)(kx[b][j] >> 16);
+      }
+    }
+    __syncthreads();   // image zeroed / the previous block's readers done / maxima and K^T written
     // fp16(v 2^-eb) by ldexp on each value: exact, and finite for an all-zero block (eb = -128)
     const int eb = vexp_step(max(max(vmx[0], vmx[1]), max(vmx[2], vmx[3])) << 16);
+    float* __restrict__ rec = stats + ((size_t)bh * nb64 + blk) * SW;
+    // k k^T and the k-sums first, so that the record's last writes do not wait for the V^T copy
+    if (w == NWV % 4) {
+      const int nn = lane & 31, h = lane >> 5;
+      f32x16 acc = splat16(0.f);
+#pragma unroll
+      for (int k0 = 0; k0 < BN; k0 += 16) {
+        const u32x4 x = nn < 16 ? *reinterpret_cast<const u32x4*>(&kt[nn * KTS + k0 + 8 * h]) : (u32x4){0u, 0u, 0u, 0u};
+        const u32 one = nn == 16 ? 0x3f803f80u : 0u;   // bf16 (1, 1)
+        acc = mfma32x32x16(x, nn < 16 ? x : (u32x4){one, one, one, one}, acc);
+      }
+      // lane: column nn, rows c32_row(i, h) (< 16 for i < 8)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int a = c32_row(i, h);
+        if (nn < 16 && a <= nn) rec[DV + kStatK2 + 16 * a - a * (a - 1) / 2 + nn - a] = a == nn ? acc[i] : 2.f * acc[i];
+        if (nn == 16) rec[DV + kStatK1 + a] = acc[i];
+      }
+      if (lane < 8) rec[DV + kStatK2 + kTri + lane] = lane == 0 ? (float)eb : 0.f;
+    }
     float part[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -126,14 +154,6 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
       part[e] = f0 + f1;   // zero for threads past NT (they loaded nothing)
       if (tid < NT)
         img[(col + e) * (ROW / 2) + kp] = pack_f16x2(__builtin_ldexpf(f0, -eb), __builtin_ldexpf(f1, -eb));
-    }
-    // K^T: thread t < 128 holds dims 8 (t & 1) .. +7 of key t / 2
-    if (tid < 128) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        kt[(8 * (tid & 1) + 2 * j) * KTS + (tid >> 1)] = (uint16_t)(kx[b][j] & 0xffffu);
-        kt[(8 * (tid & 1) + 2 * j + 1) * KTS + (tid >> 1)] = (uint16_t)(kx[b][j] >> 16);
-      }
     }
     // column sums over the lanes of this column group (lane bits log2(CPR) .. 5): each exchange
     // keeps the half of the lane's columns that its bit selects and adds the partner's copy of
@@ -164,30 +184,11 @@ __global__ __launch_bounds__(256) void par_pack_kernel(const uint16_t* __restric
     __syncthreads();
     u32* dst = reinterpret_cast<u32*>(vt + ((size_t)bh * nb64 + blk) * (IMG / 2));
     for (int i = tid; i < IMG / 16; i += 256) reinterpret_cast<u32x4*>(dst)[i] = reinterpret_cast<const u32x4*>(img)[i];
-    float* __restrict__ rec = stats + ((size_t)bh * nb64 + blk) * SW;
     if (tid < DV) {
       float t = 0.f;
 #pragma unroll
       for (int i = 0; i < NWV; ++i) t += csum[i][tid];
       rec[tid] = t;
-    }
-    if (w == NWV % 4) {
-      const int nn = lane & 31, h = lane >> 5;
-      f32x16 acc = splat16(0.f);
-#pragma unroll
-      for (int k0 = 0; k0 < BN; k0 += 16) {
-        const u32x4 x = nn < 16 ? *reinterpret_cast<const u32x4*>(&kt[nn * KTS + k0 + 8 * h]) : (u32x4){0u, 0u, 0u, 0u};
-        const u32 one = nn == 16 ? 0x3f803f80u : 0u;   // bf16 (1, 1)
-        acc = mfma32x32x16(x, nn < 16 ? x : (u32x4){one, one, one, one}, acc);
-      }
-      // lane: column nn, rows c32_row(i, h) (< 16 for i < 8)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int a = c32_row(i, h);
-        if (nn < 16 && a <= nn) rec[DV + kStatK2 + 16 * a - a * (a - 1) / 2 + nn - a] = a == nn ? acc[i] : 2.f * acc[i];
-        if (nn == 16) rec[DV + kStatK1 + a] = acc[i];
-      }
-      if (lane < 8) rec[DV + kStatK2 + kTri + lane] = lane == 0 ? (float)eb : 0.f;
     }
   }
 }
