@@ -97,6 +97,27 @@ def test_general_long_d64():
         assert e < TOL
 
 
+def test_general_d64_many_heads():
+    """B2 H16 N4096 d64 dv64 (the reference's chunked head dim over 32 heads): more state
+    work-groups than CUs, so two share a CU and the sweep alternates their wave priorities.
+    The first 1024 rows of every head against the dense fp64 oracle and rows across the later
+    segments of every head against fp64 rows."""
+    K = _kernels()
+    B, H, N = 2, 16, 4096
+    q, k, v = rand_qkv(B, H, N, 64, 64, seed=41, dtype=torch.bfloat16)
+    y = K.based_chunked(*to_dev(q, k, v), out_dtype=torch.float32).cpu()
+    n = 1024
+    want, _, _ = ref.based_dense(q[:, :, :n], k[:, :, :n], v[:, :, :n])
+    e0 = max(head_errs(y[:, :, :n], want))
+    rows = torch.tensor([1500, 2047, 2048, 3000, 3583, 3584, N - 1])
+    e1 = 0.0
+    for b in range(B):
+        for h in range(H):
+            e1 = max(e1, ref.rel_err(y[b, h, rows], rows_fp64(q, k, v, b, h, rows)))
+    print(f"general d64 B2 H16 N4096: prefix rows err={e0:.3e}, later rows err={e1:.3e}")
+    assert e0 < TOL and e1 < TOL
+
+
 def test_solution_takes_general_path_for_long_sequences():
     """solution() at d = 32 from GENERAL_CHUNKED_MIN_T tokens runs the segment-state path
     (equal to chunked_based_attn) and matches fp64 rows; below it the fused kernel."""
