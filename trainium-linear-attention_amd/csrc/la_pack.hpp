@@ -56,9 +56,10 @@ __device__ __forceinline__ int vexp_step(u32 absmax_f32_bits) {
 //  * column sums of V from the same registers: a butterfly over the lanes of one column group
 //    (each exchange halves the columns a lane carries, 7 shuffles for 8 columns), then the
 //    waves through LDS;
-//  * k sums and the k k^T triangle from one 32x32x16 MFMA chain over the 64 keys (wave 0):
-//    A = K^T (rows 16..31 zero), B = K with a column of ones at 16, so C[a][b] = (k k^T)[a][b]
-//    and C[a][16] = k1[a]; K^T sits in LDS as rows of keys, so each operand is one 16-byte read.
+//  * k sums and the k k^T triangle from one 32x32x16 MFMA chain over the 64 keys (wave
+//    NWV % 4, first, beside the other waves' V conversion): A = K^T (rows 16..31 zero), B = K
+//    with a column of ones at 16, so C[a][b] = (k k^T)[a][b] and C[a][16] = k1[a]; K^T sits in
+//    LDS as rows of keys, so each operand is one 16-byte read.
 constexpr int PPW = 1;   // blocks per pack work-group
 constexpr int KTS = BN + 8;   // K^T row stride (halves): 144 bytes, the operand reads on distinct banks
 
