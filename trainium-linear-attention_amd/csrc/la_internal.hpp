@@ -143,7 +143,7 @@ size_t decode_workspace_bytes(long long BH, int d, int dv);
 // reverse order, so that the CU holding the heaviest block also holds the lightest of the round
 // and every CU starts with the same work: B2 H16 N8192 d16 dv64 whole forward 189.2 -> 185.4 us,
 // B2 H16 N4096 68.7 -> 66.6 us, B1 H16 N8192 115.5 -> 112.7 us (one process).
-__device__ __forceinline__ void map_causal_block(int wg, int BH, int nqb, int& bh, int& qb, int pair_cus = 0) {
+__host__ __device__ __forceinline__ void map_causal_block(int wg, int BH, int nqb, int& bh, int& qb, int pair_cus = 0) {
   if ((BH & 7) == 0) {
     const int x = wg & 7, hpx = BH >> 3;
     int slot = wg >> 3;
