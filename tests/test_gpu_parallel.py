@@ -146,6 +146,19 @@ def test_parallel_256_query_orders_all_rows(B, H, N):
     assert e < TOL_BF16
 
 
+def test_fp32_tiled_kernel_b2_h16_n8192_all_rows():
+    """fp32 B2 H16 N8192 d16 dv64 (the tiled three-term kernel, two work-groups per CU in the
+    paired first-round order): every row of every head against the oracle's fp64 chunk
+    recurrence at the fp32 bar."""
+    K = _kernels()
+    q, k, v = ref.make_inputs(2, 16, 8192, 16, 64, torch.float32, seed=8)
+    y = K.based_parallel(*to_dev(q, k, v), out_dtype=torch.float32).cpu()
+    want = ref.based_chunked(q, k, v, chunk=512, dtype=torch.float64)
+    e = max(head_errs(y, want))
+    print(f"fp32 tiled B2 H16 N8192 all rows: worst head err={e:.3e}")
+    assert e < TOL_F32
+
+
 def test_dtype_and_layout_handling():
     K = _kernels()
     q, k, v = rand_qkv(1, 2, 100, 16, 32, seed=9, dtype=torch.float16)
