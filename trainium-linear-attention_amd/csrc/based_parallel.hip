@@ -450,6 +450,9 @@ void based_parallel_bf16_kernel(const ParallelParams p) {
           for (int qt = 0; qt < QT; ++qt) acc[qt][mt] = mfma32x32x16_f16(vf, pf[u][qt][m], acc[qt][mt]);
         }
     };
+    // scheduling hint: interleave the MFMAs with the VALU and LDS work around them (whole
+    // forward at B2 H16 N2048 31.66 -> 31.09 us, B2 H16 N8192 182.1 -> 181.5 us in one process)
+    __builtin_amdgcn_iglp_opt(0);
     S(0);
     S(1);
     issue_unit(cb0, 0);
