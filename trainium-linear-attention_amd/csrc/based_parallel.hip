@@ -33,9 +33,10 @@
 // S^T = K Q^T, so the score accumulator layout is directly the B operand layout of the PV
 // MFMA (no cross-lane shuffles).
 //
-// Staging, packed path (d = 16, dv % 8 == 0, dv <= 64, bf16): a pre-pass (vt_pack_kernel)
+// Staging, packed path (d = 16, dv % 8 == 0, dv <= 64, bf16): a pre-pass (par_pack_kernel)
 // writes V once as fp16 V^T blocks in exactly the LDS layout into a caller workspace, with the
-// per-block column sums of V (prefix-summed by colsum_scan_kernel).  The
+// per-block statistics (column sums of V, k sums, k k^T; prefix-summed over blocks by
+// stats_scan_kernel, which also settles the head's V exponent).  The
 // main kernel then copies K rows and V^T blocks global -> LDS with buffer_load ... lds (no
 // staging registers, no conversion; K rows past N read as zero) into NRAW stages, NRAW - 2
 // blocks ahead, and synchronises the work-group once per two blocks.  Barriers are plain
